@@ -1,0 +1,621 @@
+// GQA flash-decode over 8-bit affine KV (MLX layout) and over fp16/bf16 KV, split-K.
+//
+// Reference behaviour: locals/qkv.py:213-249 (attend: one query a row, keys
+// [start[b], n) of whole-buffer (words, scales, biases) triples read in place,
+// softmax with a per-head sink, split into key blocks joined by a log-sum-exp
+// pass, qkv.py:30-87 and 179-208) and locals/attention.py:200-224
+// (ragged_attention: row r reads KV slot slots[r], keys [0, nkeys[r]), no sink,
+// 0 for an empty row).
+//
+// MI355X design (one pass-1 workgroup = 4 waves = one (row, kv head, head slice,
+// key chunk); each wave streams a quarter of the chunk in tiles of 16 keys):
+//  * Q K^T on MFMA 16x16x16 f16: A = 16 keys x 16 dims of codes turned into exact
+//    fp16 (1024 + code) by one v_perm per two codes, B = Q^T with the G query
+//    heads of the kv head in the 16 columns (one key tile is read once for all of
+//    them).  Two accumulators, one per 64-dim group, so the per-(key, group)
+//    scale and bias apply after the product:
+//        s = sum_g sc_g * (acc_g - 1024 Qs_g) + b_g * Qs_g,   Qs_g = sum of q over g.
+//  * The score tile comes out of the MFMA as D[key][head]; that is exactly the A
+//    layout of the P V product (lane = head, 4 consecutive keys), so P never
+//    moves between lanes.  P V on MFMA: A = w = p * vscale (per key and group)
+//    split into fp16 hi + lo (relative error 2^-21, i.e. fp32-grade weights),
+//    B = V codes as 1024 + code, transposed from 4 keys' words by v_perm.  The
+//    bias and the 1024 offset go into one fp32 accumulator per (head, group):
+//        o_d = sum_t w_t (1024 + c_td) + sum_t (p_t b_t - 1024 w_t).
+//  * Online softmax in base 2, lazily rescaled: the running max only moves when
+//    a tile's max exceeds it by more than 2^6, so p <= 64 and w stays in fp16
+//    range; the rescale is a wave-uniform branch taken a handful of times.
+//  * The 4 waves' partials are joined in LDS into one (m, l, o[128]) per (row,
+//    head, chunk); pass 2 joins the chunks with the sink.
+// Loads: per 16-key tile a lane issues 2 x 128-bit loads of K codes, 8 x 32-bit
+// loads of V codes (4 keys x 2 groups) and 4 x 128-bit loads of the four keys'
+// scale/bias pairs; the next tile's loads are in flight while a tile computes.
+
+#include "lcl_common.h"
+#include "locals_amd.h"
+
+namespace lcl {
+
+constexpr int kHD = 128;
+constexpr int kWaves = 4;
+constexpr float kRescaleThr = 6.0f;
+
+struct DecodeParams {
+  const void* q;       // (R, H, HD), dtype qdt
+  const uint32_t* kw;  // 8-bit: (rows, KVH, cap, 32) words
+  const void* ks;
+  const void* kb;      // 8-bit: (rows, KVH, cap, 2) scales / biases, dtype sdt
+  const uint32_t* vw;
+  const void* vs;
+  const void* vb;
+  const void* kf;      // 16-bit KV: (rows, KVH, cap, HD), dtype sdt
+  const void* vf;
+  const int32_t* start;  // (R,) first key of each row, or null
+  const int32_t* slots;  // (R,) KV row of each query row, or null (row r -> r)
+  const int32_t* nkeys;  // (R,) end of each row, or null (n)
+  float* pm;
+  float* pl;
+  float* po;
+  int n, cap, H, KVH, G, nslices, nchunks, chunk;
+  int kv_rows;  // rows of the KV buffers (B, or n_slots); a slot outside is clamped
+  float scale_log2;
+  const float* scale_dev;  // if set, the scale is read from device memory (times log2 e in the kernel)
+  int qdt, sdt;
+};
+
+struct CombineParams {
+  const float* pm;
+  const float* pl;
+  const float* po;
+  const float* sinks;  // (H,) natural-log units, or null
+  void* out;           // (R, H, HD), dtype odt
+  const int32_t* start;
+  const int32_t* nkeys;
+  int n, cap, H, nchunks, chunk, odt;
+};
+
+__device__ __forceinline__ void row_range(const int32_t* start, const int32_t* nkeys, int n, int cap, int r, int& lo,
+                                          int& hi) {
+  lo = start ? max(start[r], 0) : 0;
+  hi = nkeys ? min(max(nkeys[r], 0), cap) : n;
+}
+
+// Q^T as the B operand: lane (head c16, quad q4) holds q[head][dim(j, q4, i)], i = 0..3
+__device__ __forceinline__ void load_q_cols(const DecodeParams& p, size_t qrow, bool real, int dim0, _Float16 (&qh)[4],
+                                            float& qsum) {
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const float v = real ? load_as_f32(p.q, qrow * kHD + dim0 + i, p.qdt) : 0.0f;
+    qh[i] = _Float16(v);
+    qsum += float(qh[i]);
+  }
+}
+
+// ---------------------------------------------------------------- 8-bit pass 1
+template <int SDT>
+__global__ __launch_bounds__(256) void qkv_pass1_q8(DecodeParams p) {
+  const int c = blockIdx.x;
+  const int kvh = blockIdx.y / p.nslices, sl = blockIdx.y % p.nslices;
+  const int r = blockIdx.z;
+  int lo, hi;
+  row_range(p.start, p.nkeys, p.n, p.cap, r, lo, hi);
+  const int c0 = c * p.chunk;
+  if (max(lo, c0) >= min(hi, c0 + p.chunk)) return;  // uniform: no key of this row in this chunk
+
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int c16 = lane & 15, q4 = lane >> 4;
+  const int sub = p.chunk / kWaves;
+  const int tlo = max(lo, c0 + wave * sub), thi = min(hi, c0 + (wave + 1) * sub);
+  const int Gs = min(16, p.G - sl * 16);
+  const int head0 = kvh * p.G + sl * 16;
+  const int slot = p.slots ? min(max(p.slots[r], 0), p.kv_rows - 1) : r;
+  const size_t tok0 = (size_t(slot) * p.KVH + kvh) * p.cap;
+
+  // B operands of Q K^T: qb[4g + jj] = q[head c16][64g + 16q4 + 4jj + i]
+  h4 qb[8];
+  float qs0 = 0.0f, qs1 = 0.0f;
+  {
+    const bool real = c16 < Gs;
+    const size_t qrow = size_t(r) * p.H + head0 + (real ? c16 : 0);
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      _Float16 t[4];
+      float& qs = j < 4 ? qs0 : qs1;
+      load_q_cols(p, qrow, real, 64 * (j >> 2) + 16 * q4 + 4 * (j & 3), t, qs);
+      qb[j] = h4{t[0], t[1], t[2], t[3]};
+    }
+  }
+  qs0 += __shfl_xor(qs0, 16);
+  qs0 += __shfl_xor(qs0, 32);
+  qs1 += __shfl_xor(qs1, 16);
+  qs1 += __shfl_xor(qs1, 32);
+  const float z0 = 1024.0f * qs0, z1 = 1024.0f * qs1;
+
+  float m_run = -INFINITY, l_acc = 0.0f, wb0 = 0.0f, wb1 = 0.0f;
+  f4 O[8];
+#pragma unroll
+  for (int ii = 0; ii < 8; ii++) O[ii] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+
+  if (tlo < thi) {
+    const int tb0 = tlo & ~15;
+    // tile loads: K codes of key (tb + c16), the scale/bias quads and V codes of keys tb + 4q4 + k
+    auto load_tile = [&](int tb, uint4& ka, uint4& kc, uint4& ksc, uint4& kbi, uint4& vsc, uint4& vbi,
+                         uint32_t (&vd)[8]) {
+      const uint32_t* krow = p.kw + (tok0 + tb + c16) * 32;
+      ka = *reinterpret_cast<const uint4*>(krow + 4 * q4);
+      kc = *reinterpret_cast<const uint4*>(krow + 16 + 4 * q4);
+      const size_t ts = tok0 + tb + 4 * q4;
+      ksc = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(p.ks) + ts * 2);
+      kbi = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(p.kb) + ts * 2);
+      vsc = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(p.vs) + ts * 2);
+      vbi = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(p.vb) + ts * 2);
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        vd[2 * k] = p.vw[(ts + k) * 32 + c16];
+        vd[2 * k + 1] = p.vw[(ts + k) * 32 + 16 + c16];
+      }
+    };
+    uint4 ka, kc, ksc, kbi, vsc, vbi;
+    uint32_t vd[8];
+    load_tile(tb0, ka, kc, ksc, kbi, vsc, vbi, vd);
+    for (int tb = tb0; tb < thi; tb += 16) {
+      uint4 nka, nkc, nksc, nkbi, nvsc, nvbi;
+      uint32_t nvd[8];
+      const bool more = tb + 16 < thi;
+      if (more) load_tile(tb + 16, nka, nkc, nksc, nkbi, nvsc, nvbi, nvd);
+
+      // ---- S^T = K Q^T, one accumulator per 64-dim group
+      f4 a0 = f4{0.0f, 0.0f, 0.0f, 0.0f}, a1 = a0;
+      a0 = mfma16(codes4_to_h4(ka.x), qb[0], a0);
+      a0 = mfma16(codes4_to_h4(ka.y), qb[1], a0);
+      a0 = mfma16(codes4_to_h4(ka.z), qb[2], a0);
+      a0 = mfma16(codes4_to_h4(ka.w), qb[3], a0);
+      a1 = mfma16(codes4_to_h4(kc.x), qb[4], a1);
+      a1 = mfma16(codes4_to_h4(kc.y), qb[5], a1);
+      a1 = mfma16(codes4_to_h4(kc.z), qb[6], a1);
+      a1 = mfma16(codes4_to_h4(kc.w), qb[7], a1);
+
+      // ---- scores of keys tb + 4q4 + i for head c16 (base-2 logits)
+      const uint32_t kscw[4] = {ksc.x, ksc.y, ksc.z, ksc.w}, kbiw[4] = {kbi.x, kbi.y, kbi.z, kbi.w};
+      const uint32_t vscw[4] = {vsc.x, vsc.y, vsc.z, vsc.w}, vbiw[4] = {vbi.x, vbi.y, vbi.z, vbi.w};
+      float s[4];
+      bool valid[4];
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int t = tb + 4 * q4 + i;
+        valid[i] = t >= tlo && t < thi;
+        const float raw = half_of(kscw[i], 0, SDT) * (a0[i] - z0) + half_of(kscw[i], 1, SDT) * (a1[i] - z1) +
+                          half_of(kbiw[i], 0, SDT) * qs0 + half_of(kbiw[i], 1, SDT) * qs1;
+        s[i] = valid[i] ? raw * p.scale_log2 : -INFINITY;
+      }
+      float tmax = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
+      tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
+      tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+      const bool need = tmax > m_run + kRescaleThr;
+      if (__any(need)) {
+        const float corr = need ? (m_run == -INFINITY ? 0.0f : fast_exp2(m_run - tmax)) : 1.0f;
+        if (need) m_run = tmax;
+        l_acc *= corr;
+        wb0 *= corr;
+        wb1 *= corr;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          const float ci = __shfl(corr, 4 * q4 + i);
+#pragma unroll
+          for (int ii = 0; ii < 8; ii++) O[ii][i] *= ci;
+        }
+      }
+      float w0[4], w1[4];
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const float pr = valid[i] ? fast_exp2(s[i] - m_run) : 0.0f;
+        l_acc += pr;
+        w0[i] = valid[i] ? pr * half_of(vscw[i], 0, SDT) : 0.0f;
+        w1[i] = valid[i] ? pr * half_of(vscw[i], 1, SDT) : 0.0f;
+        const float pb0 = valid[i] ? pr * half_of(vbiw[i], 0, SDT) : 0.0f;
+        const float pb1 = valid[i] ? pr * half_of(vbiw[i], 1, SDT) : 0.0f;
+        wb0 += pb0 - 1024.0f * w0[i];
+        wb1 += pb1 - 1024.0f * w1[i];
+      }
+      uint32_t h0a, l0a, h0b, l0b, h1a, l1a, h1b, l1b;
+      split_h2(w0[0], w0[1], h0a, l0a);
+      split_h2(w0[2], w0[3], h0b, l0b);
+      split_h2(w1[0], w1[1], h1a, l1a);
+      split_h2(w1[2], w1[3], h1b, l1b);
+      const h4 A0h = pack_h4(h0a, h0b), A0l = pack_h4(l0a, l0b);
+      const h4 A1h = pack_h4(h1a, h1b), A1l = pack_h4(l1a, l1b);
+
+      // ---- O[head][64g + 4c16 + jj] += sum_k w[head][k] (1024 + V[tb + 4q4 + k][...])
+#pragma unroll
+      for (int g = 0; g < 2; g++) {
+        const uint32_t x01 = __builtin_amdgcn_perm(vd[2 + g], vd[g], 0x05010400u);
+        const uint32_t y01 = __builtin_amdgcn_perm(vd[2 + g], vd[g], 0x07030602u);
+        const uint32_t x23 = __builtin_amdgcn_perm(vd[6 + g], vd[4 + g], 0x05010400u);
+        const uint32_t y23 = __builtin_amdgcn_perm(vd[6 + g], vd[4 + g], 0x07030602u);
+        const h4 b0 = pack_h4(codes_to_h2(x01, 0x00050004u), codes_to_h2(x23, 0x00050004u));
+        const h4 b1 = pack_h4(codes_to_h2(x01, 0x00070006u), codes_to_h2(x23, 0x00070006u));
+        const h4 b2 = pack_h4(codes_to_h2(y01, 0x00050004u), codes_to_h2(y23, 0x00050004u));
+        const h4 b3 = pack_h4(codes_to_h2(y01, 0x00070006u), codes_to_h2(y23, 0x00070006u));
+        const h4 Ah = g ? A1h : A0h, Al = g ? A1l : A0l;
+        O[4 * g + 0] = mfma16(Al, b0, mfma16(Ah, b0, O[4 * g + 0]));
+        O[4 * g + 1] = mfma16(Al, b1, mfma16(Ah, b1, O[4 * g + 1]));
+        O[4 * g + 2] = mfma16(Al, b2, mfma16(Ah, b2, O[4 * g + 2]));
+        O[4 * g + 3] = mfma16(Al, b3, mfma16(Ah, b3, O[4 * g + 3]));
+      }
+      if (more) {
+        ka = nka; kc = nkc; ksc = nksc; kbi = nkbi; vsc = nvsc; vbi = nvbi;
+#pragma unroll
+        for (int k = 0; k < 8; k++) vd[k] = nvd[k];
+      }
+    }
+  }
+
+  // ---- join the 4 waves in LDS, one part per (row, head, chunk)
+  l_acc += __shfl_xor(l_acc, 16);
+  l_acc += __shfl_xor(l_acc, 32);
+  wb0 += __shfl_xor(wb0, 16);
+  wb0 += __shfl_xor(wb0, 32);
+  wb1 += __shfl_xor(wb1, 16);
+  wb1 += __shfl_xor(wb1, 32);
+  __shared__ float s_m[kWaves][16], s_l[kWaves][16];
+  __shared__ float s_o[kWaves][16][kHD];
+  if (q4 == 0) {
+    s_m[wave][c16] = m_run;
+    s_l[wave][c16] = l_acc;
+  }
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const float b0 = __shfl(wb0, 4 * q4 + i), b1 = __shfl(wb1, 4 * q4 + i);
+#pragma unroll
+    for (int ii = 0; ii < 8; ii++) s_o[wave][4 * q4 + i][64 * (ii >> 2) + 4 * c16 + (ii & 3)] = O[ii][i] + (ii < 4 ? b0 : b1);
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < Gs * kHD; e += 256) {
+    const int h = e >> 7, d = e & (kHD - 1);
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kWaves; w++) M = fmaxf(M, s_m[w][h]);
+    float L = 0.0f, o = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kWaves; w++) {
+      const float f = s_m[w][h] == -INFINITY ? 0.0f : fast_exp2(s_m[w][h] - M);
+      L += f * s_l[w][h];
+      o += f * s_o[w][h][d];
+    }
+    const size_t part = (size_t(r) * p.H + head0 + h) * p.nchunks + c;
+    p.po[part * kHD + d] = o;
+    if (d == 0) {
+      p.pm[part] = M;
+      p.pl[part] = L;
+    }
+  }
+}
+
+// ------------------------------------------------------------ 16-bit pass 1
+// K/V of dtype KDT (fp16 or bf16) in (rows, KVH, cap, 128).  Q K^T: lane (key
+// c16, quad q4) supplies dims 32q4 + 4j + i of its key for MFMA j; P V: N-tile ii
+// column n is dim 8n + ii, so a lane reads 16 contiguous bytes of each of its 4 keys.
+template <int KDT>
+__global__ __launch_bounds__(256) void ragged_pass1_16(DecodeParams p) {
+  const int c = blockIdx.x;
+  const int kvh = blockIdx.y / p.nslices, sl = blockIdx.y % p.nslices;
+  const int r = blockIdx.z;
+  int lo, hi;
+  row_range(p.start, p.nkeys, p.n, p.cap, r, lo, hi);
+  const int c0 = c * p.chunk;
+  if (max(lo, c0) >= min(hi, c0 + p.chunk)) return;
+
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int c16 = lane & 15, q4 = lane >> 4;
+  const int sub = p.chunk / kWaves;
+  const int tlo = max(lo, c0 + wave * sub), thi = min(hi, c0 + (wave + 1) * sub);
+  const int Gs = min(16, p.G - sl * 16);
+  const int head0 = kvh * p.G + sl * 16;
+  const int slot = p.slots ? min(max(p.slots[r], 0), p.kv_rows - 1) : r;
+  const size_t tok0 = (size_t(slot) * p.KVH + kvh) * p.cap;
+  const uint16_t* K = static_cast<const uint16_t*>(p.kf);
+  const uint16_t* V = static_cast<const uint16_t*>(p.vf);
+  const float scale_log2 = p.scale_dev ? p.scale_dev[0] * kLog2e : p.scale_log2;
+
+  uint32_t qb[8][2];
+  {
+    const bool real = c16 < Gs;
+    const size_t qrow = size_t(r) * p.H + head0 + (real ? c16 : 0);
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      uint32_t bits[4];
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const float v = real ? load_as_f32(p.q, qrow * kHD + 32 * q4 + 4 * j + i, p.qdt) : 0.0f;
+        bits[i] = KDT == DT_BF16 ? f32_to_bf16_bits(v) : __builtin_bit_cast(uint16_t, _Float16(v));
+      }
+      qb[j][0] = bits[0] | (bits[1] << 16);
+      qb[j][1] = bits[2] | (bits[3] << 16);
+    }
+  }
+
+  float m_run = -INFINITY, l_acc = 0.0f;
+  f4 O[8];
+#pragma unroll
+  for (int ii = 0; ii < 8; ii++) O[ii] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+
+  if (tlo < thi) {
+    const int tb0 = tlo & ~15;
+    auto load_tile = [&](int tb, uint4 (&kd)[4], uint4 (&vd)[4]) {
+      const uint16_t* krow = K + (tok0 + tb + c16) * kHD + 32 * q4;
+#pragma unroll
+      for (int u = 0; u < 4; u++) kd[u] = *reinterpret_cast<const uint4*>(krow + 8 * u);
+#pragma unroll
+      for (int k = 0; k < 4; k++) vd[k] = *reinterpret_cast<const uint4*>(V + (tok0 + tb + 4 * q4 + k) * kHD + 8 * c16);
+    };
+    uint4 kd[4], vd[4];
+    load_tile(tb0, kd, vd);
+    for (int tb = tb0; tb < thi; tb += 16) {
+      uint4 nkd[4], nvd[4];
+      const bool more = tb + 16 < thi;
+      if (more) load_tile(tb + 16, nkd, nvd);
+      f4 a = f4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int j = 0; j < 8; j++) {
+        const uint4 u = kd[j >> 1];
+        const uint32_t w0 = (j & 1) ? u.z : u.x, w1 = (j & 1) ? u.w : u.y;
+        if (KDT == DT_BF16) a = mfma16bf(pack_s4(w0, w1), pack_s4(qb[j][0], qb[j][1]), a);
+        else a = mfma16(pack_h4(w0, w1), pack_h4(qb[j][0], qb[j][1]), a);
+      }
+      float s[4];
+      bool valid[4];
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int t = tb + 4 * q4 + i;
+        valid[i] = t >= tlo && t < thi;
+        s[i] = valid[i] ? a[i] * scale_log2 : -INFINITY;
+      }
+      float tmax = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
+      tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
+      tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+      const bool need = tmax > m_run + kRescaleThr;
+      if (__any(need)) {
+        const float corr = need ? (m_run == -INFINITY ? 0.0f : fast_exp2(m_run - tmax)) : 1.0f;
+        if (need) m_run = tmax;
+        l_acc *= corr;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          const float ci = __shfl(corr, 4 * q4 + i);
+#pragma unroll
+          for (int ii = 0; ii < 8; ii++) O[ii][i] *= ci;
+        }
+      }
+      float pr[4];
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        pr[i] = valid[i] ? fast_exp2(s[i] - m_run) : 0.0f;
+        l_acc += pr[i];
+      }
+      uint32_t ha, la, hb, lb;
+      if (KDT == DT_BF16) {
+        split_bf2(pr[0], pr[1], ha, la);
+        split_bf2(pr[2], pr[3], hb, lb);
+      } else {
+        split_h2(pr[0], pr[1], ha, la);
+        split_h2(pr[2], pr[3], hb, lb);
+      }
+      const uint32_t vw[4][4] = {{vd[0].x, vd[0].y, vd[0].z, vd[0].w},
+                                 {vd[1].x, vd[1].y, vd[1].z, vd[1].w},
+                                 {vd[2].x, vd[2].y, vd[2].z, vd[2].w},
+                                 {vd[3].x, vd[3].y, vd[3].z, vd[3].w}};
+#pragma unroll
+      for (int ii = 0; ii < 8; ii++) {
+        const uint32_t sel = (ii & 1) ? 0x07060302u : 0x05040100u;
+        const uint32_t b01 = __builtin_amdgcn_perm(vw[1][ii >> 1], vw[0][ii >> 1], sel);
+        const uint32_t b23 = __builtin_amdgcn_perm(vw[3][ii >> 1], vw[2][ii >> 1], sel);
+        if (KDT == DT_BF16) {
+          O[ii] = mfma16bf(pack_s4(ha, hb), pack_s4(b01, b23), O[ii]);
+          O[ii] = mfma16bf(pack_s4(la, lb), pack_s4(b01, b23), O[ii]);
+        } else {
+          O[ii] = mfma16(pack_h4(ha, hb), pack_h4(b01, b23), O[ii]);
+          O[ii] = mfma16(pack_h4(la, lb), pack_h4(b01, b23), O[ii]);
+        }
+      }
+      if (more) {
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+          kd[u] = nkd[u];
+          vd[u] = nvd[u];
+        }
+      }
+    }
+  }
+
+  l_acc += __shfl_xor(l_acc, 16);
+  l_acc += __shfl_xor(l_acc, 32);
+  __shared__ float s_m[kWaves][16], s_l[kWaves][16];
+  __shared__ float s_o[kWaves][16][kHD];
+  if (q4 == 0) {
+    s_m[wave][c16] = m_run;
+    s_l[wave][c16] = l_acc;
+  }
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+#pragma unroll
+    for (int ii = 0; ii < 8; ii++) s_o[wave][4 * q4 + i][8 * c16 + ii] = O[ii][i];
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < Gs * kHD; e += 256) {
+    const int h = e >> 7, d = e & (kHD - 1);
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kWaves; w++) M = fmaxf(M, s_m[w][h]);
+    float L = 0.0f, o = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kWaves; w++) {
+      const float f = s_m[w][h] == -INFINITY ? 0.0f : fast_exp2(s_m[w][h] - M);
+      L += f * s_l[w][h];
+      o += f * s_o[w][h][d];
+    }
+    const size_t part = (size_t(r) * p.H + head0 + h) * p.nchunks + c;
+    p.po[part * kHD + d] = o;
+    if (d == 0) {
+      p.pm[part] = M;
+      p.pl[part] = L;
+    }
+  }
+}
+
+// ------------------------------------------------------------------- pass 2
+// One workgroup per (row, head): 4 waves each fold every 4th chunk (online, base
+// 2), joined in LDS with the sink: M = max(sink, m_v), L = 2^(sink-M) + sum l_v 2^(m_v-M),
+// out = sum o_v 2^(m_v-M) / L (locals/qkv.py:179-208).  No key and no sink: 0.
+__global__ __launch_bounds__(256) void decode_combine(CombineParams p) {
+  const int rh = blockIdx.x, r = rh / p.H, head = rh % p.H;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  int lo, hi;
+  row_range(p.start, p.nkeys, p.n, p.cap, r, lo, hi);
+  int cl = 0, ch = 0;
+  if (hi > lo) {
+    cl = lo / p.chunk;
+    ch = (hi + p.chunk - 1) / p.chunk;
+  }
+  float M = -INFINITY, L = 0.0f, o0 = 0.0f, o1 = 0.0f;
+  const size_t base = size_t(rh) * p.nchunks;
+  for (int c = cl + wave; c < ch; c += kWaves) {
+    const float mc = p.pm[base + c], lc = p.pl[base + c];
+    const float2 oc = *reinterpret_cast<const float2*>(p.po + (base + c) * kHD + 2 * lane);
+    if (mc == -INFINITY) continue;
+    const float Mn = fmaxf(M, mc);
+    const float fo = M == -INFINITY ? 0.0f : fast_exp2(M - Mn), fn = fast_exp2(mc - Mn);
+    L = L * fo + lc * fn;
+    o0 = o0 * fo + oc.x * fn;
+    o1 = o1 * fo + oc.y * fn;
+    M = Mn;
+  }
+  __shared__ float s_m[kWaves], s_l[kWaves], s_o[kWaves][kHD];
+  if (lane == 0) {
+    s_m[wave] = M;
+    s_l[wave] = L;
+  }
+  s_o[wave][2 * lane] = o0;
+  s_o[wave][2 * lane + 1] = o1;
+  __syncthreads();
+  if (wave) return;
+  const float sink = p.sinks ? p.sinks[head] * kLog2e : -INFINITY;
+  float Mt = sink;
+#pragma unroll
+  for (int w = 0; w < kWaves; w++) Mt = fmaxf(Mt, s_m[w]);
+  float r0 = 0.0f, r1 = 0.0f;
+  if (Mt != -INFINITY) {
+    float Lt = sink == -INFINITY ? 0.0f : fast_exp2(sink - Mt);
+#pragma unroll
+    for (int w = 0; w < kWaves; w++) {
+      const float f = s_m[w] == -INFINITY ? 0.0f : fast_exp2(s_m[w] - Mt);
+      Lt += s_l[w] * f;
+      r0 += s_o[w][2 * lane] * f;
+      r1 += s_o[w][2 * lane + 1] * f;
+    }
+    r0 /= Lt;
+    r1 /= Lt;
+  }
+  const size_t ob = size_t(rh) * kHD + 2 * lane;
+  store_from_f32(p.out, ob, r0, p.odt);
+  store_from_f32(p.out, ob + 1, r1, p.odt);
+}
+
+}  // namespace lcl
+
+using namespace lcl;
+
+static int pick_chunk(int block, int extent) {
+  if (block > 0) return block;
+  (void)extent;
+  return 512;
+}
+
+static size_t ws_bytes_for(int R, int H, int nchunks) {
+  return size_t(R) * H * nchunks * (2 + kHD) * sizeof(float);
+}
+
+extern "C" {
+
+size_t lcl_decode_workspace_bytes(int R, int H, int extent, int block) {
+  const int chunk = pick_chunk(block, extent);
+  const int nchunks = extent > 0 ? (extent + chunk - 1) / chunk : 1;
+  return ws_bytes_for(R, H, nchunks);
+}
+
+int lcl_qkv_attend(const void* q, int qdt, const uint32_t* kw, const void* ks, const void* kb, const uint32_t* vw,
+                   const void* vs, const void* vb, int sdt, const int32_t* start, const float* sinks, float scale,
+                   int B, int H, int KVH, int hd, int cap, int n, int block, void* out, void* workspace,
+                   size_t workspace_bytes, void* stream_) {
+  hipStream_t stream = static_cast<hipStream_t>(stream_);
+  if (!q || !kw || !ks || !kb || !vw || !vs || !vb || !out) return -1;
+  if (hd != kHD) return -2;
+  if (B <= 0 || H <= 0 || KVH <= 0 || H % KVH || cap <= 0 || cap % 16 || n < 0 || n > cap) return -1;
+  if (block < 0 || block % 64) return -1;
+  if ((qdt != DT_F16 && qdt != DT_BF16 && qdt != DT_F32) || (sdt != DT_F16 && sdt != DT_BF16)) return -1;
+  const int chunk = pick_chunk(block, n);
+  const int nchunks = n > 0 ? (n + chunk - 1) / chunk : 1;
+  if (!workspace || workspace_bytes < ws_bytes_for(B, H, nchunks)) return -3;
+  DecodeParams p{};
+  p.q = q;
+  p.kw = kw; p.ks = ks; p.kb = kb;
+  p.vw = vw; p.vs = vs; p.vb = vb;
+  p.start = start;
+  float* ws = static_cast<float*>(workspace);
+  const size_t np = size_t(B) * H * nchunks;
+  p.pm = ws;
+  p.pl = ws + np;
+  p.po = ws + 2 * np;
+  p.n = n; p.cap = cap; p.H = H; p.KVH = KVH; p.G = H / KVH; p.kv_rows = B;
+  p.nslices = (p.G + 15) / 16;
+  p.nchunks = nchunks; p.chunk = chunk;
+  p.scale_log2 = scale * kLog2e;
+  p.qdt = qdt; p.sdt = sdt;
+  if (n > 0) {
+    const dim3 grid(nchunks, KVH * p.nslices, B);
+    if (sdt == DT_BF16) hipLaunchKernelGGL(qkv_pass1_q8<DT_BF16>, grid, dim3(256), 0, stream, p);
+    else hipLaunchKernelGGL(qkv_pass1_q8<DT_F16>, grid, dim3(256), 0, stream, p);
+  }
+  CombineParams c{};
+  c.pm = p.pm; c.pl = p.pl; c.po = p.po; c.sinks = sinks; c.out = out;
+  c.start = start; c.nkeys = nullptr; c.n = n; c.cap = cap; c.H = H; c.nchunks = nchunks; c.chunk = chunk; c.odt = qdt;
+  hipLaunchKernelGGL(decode_combine, dim3(B * H), dim3(256), 0, stream, c);
+  return int(hipGetLastError());
+}
+
+int lcl_ragged_attention(const void* q, int qdt, const void* keys, const void* values, int kvdt, const int32_t* slots,
+                         const int32_t* nkeys, float scale, const float* scale_dev, int R, int H, int n_slots, int Hkv, int hd, int cap,
+                         int block, void* out, void* workspace, size_t workspace_bytes, void* stream_) {
+  hipStream_t stream = static_cast<hipStream_t>(stream_);
+  if (!q || !keys || !values || !slots || !nkeys || !out) return -1;
+  if (hd != kHD) return -2;
+  if (R < 0 || H <= 0 || Hkv <= 0 || H % Hkv || n_slots <= 0 || cap <= 0 || cap % 16) return -1;
+  if (block < 0 || block % 64) return -1;
+  if ((qdt != DT_F16 && qdt != DT_BF16 && qdt != DT_F32) || (kvdt != DT_F16 && kvdt != DT_BF16)) return -1;
+  if (R == 0) return 0;
+  const int chunk = pick_chunk(block, cap);
+  const int nchunks = (cap + chunk - 1) / chunk;
+  if (!workspace || workspace_bytes < ws_bytes_for(R, H, nchunks)) return -3;
+  DecodeParams p{};
+  p.q = q;
+  p.kf = keys; p.vf = values;
+  p.slots = slots; p.nkeys = nkeys;
+  float* ws = static_cast<float*>(workspace);
+  const size_t np = size_t(R) * H * nchunks;
+  p.pm = ws; p.pl = ws + np; p.po = ws + 2 * np;
+  p.n = cap; p.cap = cap; p.H = H; p.KVH = Hkv; p.G = H / Hkv; p.kv_rows = n_slots;
+  p.nslices = (p.G + 15) / 16;
+  p.nchunks = nchunks; p.chunk = chunk;
+  p.scale_log2 = scale * kLog2e;
+  p.scale_dev = scale_dev;
+  p.qdt = qdt; p.sdt = kvdt;
+  const dim3 grid(nchunks, Hkv * p.nslices, R);
+  if (kvdt == DT_BF16) hipLaunchKernelGGL(ragged_pass1_16<DT_BF16>, grid, dim3(256), 0, stream, p);
+  else hipLaunchKernelGGL(ragged_pass1_16<DT_F16>, grid, dim3(256), 0, stream, p);
+  CombineParams c{};
+  c.pm = p.pm; c.pl = p.pl; c.po = p.po; c.sinks = nullptr; c.out = out;
+  c.start = nullptr; c.nkeys = nkeys; c.n = cap; c.cap = cap; c.H = H; c.nchunks = nchunks; c.chunk = chunk;
+  c.odt = qdt;
+  hipLaunchKernelGGL(decode_combine, dim3(R * H), dim3(256), 0, stream, c);
+  return int(hipGetLastError());
+}
+
+}  // extern "C"

@@ -1,0 +1,107 @@
+// Shared device helpers for the gfx950 (CDNA4) attention kernels.
+//
+// Conventions used by every kernel in this directory:
+//  * wave64; MFMA v_mfma_f32_16x16x16{f16,bf16_1k} operand layout:
+//      A (16 x 16, M x K): lane l holds A[l % 16][4 * (l / 16) + i], i = 0..3
+//      B (16 x 16, K x N): lane l holds B[4 * (l / 16) + i][l % 16]
+//      D (16 x 16, M x N): lane l holds D[4 * (l / 16) + i][l % 16]
+//    (checked on an MI355X by an in-bounds probe of the builtin).
+//  * An 8-bit code c becomes the exact fp16 value 1024 + c by byte-permuting it
+//    under the exponent byte 0x64 (fp16 0x64cc == 1024 + cc); the constant 1024
+//    is folded back out in fp32 by each kernel.
+//  * Status codes: 0 ok, negative = argument error (see include/locals_amd.h),
+//    positive = hipError_t passed through.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace lcl {
+
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+typedef short s4 __attribute__((ext_vector_type(4)));
+typedef float f4 __attribute__((ext_vector_type(4)));
+
+enum Dtype { DT_F16 = 0, DT_BF16 = 1, DT_F32 = 2 };
+
+constexpr float kLog2e = 1.4426950408889634f;
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint16_t b) { return __uint_as_float(uint32_t(b) << 16); }
+__device__ __forceinline__ float f16_bits_to_f32(uint16_t b) { return float(__builtin_bit_cast(_Float16, b)); }
+
+// round-to-nearest-even float -> bf16 bits (inputs here are finite)
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float x) {
+  uint32_t u = __float_as_uint(x);
+  if ((u & 0x7f800000u) == 0x7f800000u) return uint16_t((u >> 16) | ((u & 0xffffu) ? 0x40u : 0u));
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return uint16_t(u >> 16);
+}
+
+// value of a 16-bit (or fp32) element of dtype dt
+__device__ __forceinline__ float load_as_f32(const void* p, size_t i, int dt) {
+  if (dt == DT_F16) return f16_bits_to_f32(static_cast<const uint16_t*>(p)[i]);
+  if (dt == DT_BF16) return bf16_bits_to_f32(static_cast<const uint16_t*>(p)[i]);
+  return static_cast<const float*>(p)[i];
+}
+
+__device__ __forceinline__ void store_from_f32(void* p, size_t i, float v, int dt) {
+  if (dt == DT_F16) static_cast<_Float16*>(p)[i] = _Float16(v);
+  else if (dt == DT_BF16) static_cast<uint16_t*>(p)[i] = f32_to_bf16_bits(v);
+  else static_cast<float*>(p)[i] = v;
+}
+
+// element k (0/1) of a packed pair of 16-bit values of dtype dt
+__device__ __forceinline__ float half_of(uint32_t w, int k, int dt) {
+  const uint16_t b = uint16_t(k ? (w >> 16) : (w & 0xffffu));
+  return dt == DT_BF16 ? bf16_bits_to_f32(b) : f16_bits_to_f32(b);
+}
+
+// bytes 0,1 (sel 0x00050004) or 2,3 (sel 0x00070006) of x as two fp16 values 1024 + byte
+__device__ __forceinline__ uint32_t codes_to_h2(uint32_t x, uint32_t sel) {
+  return __builtin_amdgcn_perm(x, 0x64646464u, sel);
+}
+
+__device__ __forceinline__ h4 codes4_to_h4(uint32_t x) {
+  const uint32_t lo = codes_to_h2(x, 0x00050004u), hi = codes_to_h2(x, 0x00070006u);
+  return __builtin_bit_cast(h4, (uint64_t(hi) << 32) | lo);
+}
+
+__device__ __forceinline__ h4 pack_h4(uint32_t lo, uint32_t hi) {
+  return __builtin_bit_cast(h4, (uint64_t(hi) << 32) | lo);
+}
+
+__device__ __forceinline__ s4 pack_s4(uint32_t lo, uint32_t hi) {
+  return __builtin_bit_cast(s4, (uint64_t(hi) << 32) | lo);
+}
+
+__device__ __forceinline__ f4 mfma16(h4 a, h4 b, f4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ f4 mfma16bf(s4 a, s4 b, f4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
+}
+
+// two floats -> packed fp16 pair, round toward zero (v_cvt_pkrtz_f16_f32)
+__device__ __forceinline__ uint32_t pkrtz(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(a, b));
+}
+
+// w ~= hi + lo with hi, lo fp16 (round toward zero): |w - hi - lo| <= 2^-21 |w|
+__device__ __forceinline__ void split_h2(float a, float b, uint32_t& hi, uint32_t& lo) {
+  hi = pkrtz(a, b);
+  const h2 h = __builtin_bit_cast(h2, hi);
+  lo = pkrtz(a - float(h.x), b - float(h.y));
+}
+
+// bf16 pair by truncation: hi = top 16 bits, lo = top 16 bits of the remainder
+__device__ __forceinline__ void split_bf2(float a, float b, uint32_t& hi, uint32_t& lo) {
+  const uint32_t ua = __float_as_uint(a) & 0xffff0000u, ub = __float_as_uint(b) & 0xffff0000u;
+  hi = (ua >> 16) | ub;
+  const uint32_t ra = __float_as_uint(a - __uint_as_float(ua)), rb = __float_as_uint(b - __uint_as_float(ub));
+  lo = (ra >> 16) | (rb & 0xffff0000u);
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+}  // namespace lcl

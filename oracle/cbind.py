@@ -1,0 +1,73 @@
+"""ctypes binding of ``oracle/liboracle.so`` (the C restatement) -- test infrastructure.
+
+``attend_q8`` runs the reference's two-pass split-K decode (locals/qkv.py:30-87,
+179-208, 232) in fp32 on the host cores; ``quantize`` runs MLX's affine quantizer.
+Build with ``make -C oracle`` (``__graft_entry__.build()`` does).
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+
+import numpy as np
+
+from .quant import from_f32, to_f32
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB = None
+
+
+def lib():
+    global _LIB
+    if _LIB is None:
+        path = os.path.join(_HERE, "liboracle.so")
+        if not os.path.exists(path):
+            raise RuntimeError("oracle/liboracle.so is not built (run: make -C oracle)")
+        L = ctypes.CDLL(path)
+        P = ctypes.c_void_p
+        L.orc_attend_q8.argtypes = [P] * 9 + [ctypes.c_float] + [ctypes.c_int] * 7 + [P]
+        L.orc_attend_q8.restype = ctypes.c_int
+        L.orc_quantize.argtypes = [P, ctypes.c_int64, ctypes.c_int, ctypes.c_int, ctypes.c_int, P, P, P]
+        L.orc_quantize.restype = None
+        _LIB = L
+    return _LIB
+
+
+def _p(a):
+    return ctypes.c_void_p(a.ctypes.data) if a is not None else None
+
+
+def quantize(w, dtype: str = "float16", group: int = 64, round_mode: str = "away"):
+    x = np.ascontiguousarray(to_f32(w, dtype), dtype=np.float32)
+    D = x.shape[-1]
+    rows = x.size // D
+    codes = np.empty(x.shape, dtype=np.uint8)
+    sc = np.empty(x.shape[:-1] + (D // group,), dtype=np.float32)
+    bi = np.empty_like(sc)
+    lib().orc_quantize(_p(x), rows, D, group, 0 if round_mode == "away" else 1, _p(codes), _p(sc), _p(bi))
+    words = codes.reshape(-1, D).view("<u4").reshape(x.shape[:-1] + (D // 4,))
+    return words, from_f32(sc, dtype), from_f32(bi, dtype)
+
+
+def attend_q8(q, keys, values, n: int, sinks, scale: float, start, dtype: str = "float16", block: int = 0,
+              threads: int | None = None):
+    """fp32 two-pass split-K decode on the host.  Returns float32 (B, H, 1, HD)."""
+    qf = np.ascontiguousarray(to_f32(q, dtype), dtype=np.float32)
+    B, H, _, HD = qf.shape
+    kw, ks, kb = keys
+    vw, vs, vb = values
+    KVH, cap = kw.shape[1], kw.shape[2]
+    f = lambda a: np.ascontiguousarray(to_f32(a, dtype), dtype=np.float32)  # noqa: E731
+    kw, vw = np.ascontiguousarray(kw, dtype=np.uint32), np.ascontiguousarray(vw, dtype=np.uint32)
+    ks, kb, vs, vb = f(ks), f(kb), f(vs), f(vb)
+    st = np.ascontiguousarray(start, dtype=np.int32)
+    sk = None if sinks is None else np.ascontiguousarray(to_f32(sinks, dtype), dtype=np.float32)
+    out = np.empty((B, H, HD), dtype=np.float32)
+    if threads is not None:
+        os.environ["OMP_NUM_THREADS"] = str(threads)
+    rc = lib().orc_attend_q8(_p(qf), _p(kw), _p(ks), _p(kb), _p(vw), _p(vs), _p(vb), _p(st), _p(sk),
+                             ctypes.c_float(scale), B, H, KVH, HD, cap, n, block, _p(out))
+    if rc:
+        raise ValueError(f"orc_attend_q8 failed ({rc})")
+    return out.reshape(B, H, 1, HD)
