@@ -1,0 +1,271 @@
+"""Benchmark of the batched-attention hot path on one MI355X: 8-bit-KV GQA flash-decode.
+
+    python bench.py [--steps K] [--warmup W] [--config c2|c3|c1] [--cpu-seconds S] [--no-cpu]
+
+A step is one ``qkv.attend`` over the whole batch (pass 1 + the log-sum-exp combine) with K/V already resident in
+HBM.  Workload (default, "c2"): B=16 rows, 32 query / 8 KV heads, head_dim 128, row contexts n_b ~ U[1024, 32768]
+(seeded), left-padded in one buffer of capacity n = max n_b rounded up to 256 (start_b = n - n_b), K/V ~ N(0,1) fp16
+quantized with MLX's affine 8 bits (group 64), Q ~ N(0,1) fp16, no sink.  Two independent buffer sets (2 x 1.14 GB)
+alternate so the 256 MB MALL cannot serve a step.
+
+Prints one JSON line.  ``value`` = algorithmic bytes a step (sum_b n_b * KVH * 272 + Q + O) / step time, GB/s.
+``roofline`` = the pass-1 kernel: its algorithmic bytes (K/V codes, scales, biases and Q) / its own average
+duration, timed by hipEvents recorded by its dispatch (lcl_qkv_attend_ex) inside the timed region, against the
+8 TB/s HBM peak.  ``cpu_baseline`` = the reference's two-pass split-K algorithm restated in C (oracle/, OpenMP) on
+this host's cores over a bounded sample of the same workload (kind "port").
+"""
+
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+HBM_PEAK_GBS = 8000.0
+ROOT = os.path.dirname(os.path.abspath(__file__))
+
+
+def _hip():
+    """The HIP runtime torch loaded (so events and streams are the same runtime's)."""
+    import torch  # noqa: F401
+
+    path = None
+    with open("/proc/self/maps") as f:
+        for line in f:
+            if "libamdhip64" in line:
+                path = line.split()[-1]
+                break
+    lib = ctypes.CDLL(path or "libamdhip64.so")
+    lib.hipEventCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
+    lib.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p, ctypes.c_void_p]
+    lib.hipEventDestroy.argtypes = [ctypes.c_void_p]
+    return lib
+
+
+class Events:
+    def __init__(self, n):
+        self.hip = _hip()
+        self.ev = []
+        for _ in range(n):
+            e = ctypes.c_void_p()
+            rc = self.hip.hipEventCreate(ctypes.byref(e))
+            if rc:
+                raise RuntimeError(f"hipEventCreate failed {rc}")
+            self.ev.append(e)
+
+    def ms(self, a, b):
+        t = ctypes.c_float()
+        rc = self.hip.hipEventElapsedTime(ctypes.byref(t), self.ev[a], self.ev[b])
+        if rc:
+            raise RuntimeError(f"hipEventElapsedTime failed {rc}")
+        return t.value
+
+    def close(self):
+        for e in self.ev:
+            self.hip.hipEventDestroy(e)
+
+
+def config(name: str, seed: int = 0):
+    g = np.random.default_rng(seed)
+    if name == "c2":
+        B, H, KVH = 16, 32, 8
+        nb = g.integers(1024, 32768, size=B, endpoint=True)
+        return dict(name="c2", workload="8-bit KV GQA flash-decode, mixed contexts (BASELINE config 2)",
+                    B=B, H=H, KVH=KVH, nb=nb)
+    if name == "c3":
+        return dict(name="c3", workload="long-context single-row split-K decode (BASELINE config 3)",
+                    B=1, H=16, KVH=8, nb=np.array([245760]))
+    if name == "c4d":
+        B = 15
+        return dict(name="c4d", workload="hybrid batch: the 15 decode rows (BASELINE config 4, decode part)",
+                    B=B, H=32, KVH=8, nb=g.integers(2048, 16384, size=B, endpoint=True))
+    raise SystemExit(f"unknown config {name}")
+
+
+def build_sets(cfg, nsets, dev):
+    import torch
+
+    from locals_amd import qkv
+
+    B, H, KVH = cfg["B"], cfg["H"], cfg["KVH"]
+    nb = cfg["nb"]
+    n = int(nb.max())
+    cap = (n + 255) // 256 * 256
+    start = torch.tensor(n - nb, dtype=torch.int32, device=dev)
+    gen = torch.Generator(device=dev)
+    sets = []
+    for s in range(nsets):
+        gen.manual_seed(1234 + s)
+        K = qkv._zeros(B, KVH, cap, 128, torch.float16, dev)
+        V = qkv._zeros(B, KVH, cap, 128, torch.float16, dev)
+        for b in range(B):  # a row at a time keeps the fp16 temporaries small
+            kf = torch.randn((1, KVH, cap, 128), generator=gen, device=dev, dtype=torch.float16)
+            vf = torch.randn((1, KVH, cap, 128), generator=gen, device=dev, dtype=torch.float16)
+            qkv.quantize_into(kf, vf, tuple(a[b:b + 1] for a in K), tuple(a[b:b + 1] for a in V), 0)
+        q = torch.randn((B, H, 1, 128), generator=gen, device=dev, dtype=torch.float16)
+        sets.append((q, K, V))
+    torch.cuda.synchronize()
+    return sets, start, n, cap
+
+
+def step_bytes(cfg):
+    B, H, KVH = cfg["B"], cfg["H"], cfg["KVH"]
+    kv = int(cfg["nb"].sum()) * KVH * 272
+    return kv + 2 * B * H * 128 + 2 * B * H * 128, kv + 2 * B * H * 128  # whole step, pass 1 (KV + Q)
+
+
+def cpu_baseline(cfg, sets, start, n, seconds, gpu_out):
+    """The C port of the reference algorithm on the host cores over the same inputs (set 0): whole steps repeated
+    until ``seconds`` of CPU time; also its max |difference| from the GPU's output of the same step."""
+    import torch
+
+    threads = min(16, len(os.sched_getaffinity(0)))
+    os.environ["OMP_NUM_THREADS"] = str(threads)
+    sys.path.insert(0, ROOT)
+    from oracle import cbind
+
+    q, K, V = sets[0]
+    tonp = lambda t: t.cpu().numpy()  # noqa: E731
+    qn = tonp(q)
+    Kn = (tonp(K[0]).view(np.uint32), tonp(K[1]), tonp(K[2]))
+    Vn = (tonp(V[0]).view(np.uint32), tonp(V[1]), tonp(V[2]))
+    st = tonp(start)
+    reps, t0 = 0, time.perf_counter()
+    out = None
+    while True:
+        out = cbind.attend_q8(qn, Kn, Vn, n, None, 1 / np.sqrt(128), st, threads=threads)
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= seconds:
+            break
+    per = el / reps
+    err = float(np.abs(out.astype(np.float64) - gpu_out.float().cpu().numpy()).max())
+    cpu = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    cpu = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return per, reps, threads, cpu, err
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--config", default="c2")
+    ap.add_argument("--sets", type=int, default=2)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (each GPU box here has one GPU); "
+              "run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    sys.path.insert(0, ROOT)
+    from locals_amd import _lib, qkv
+
+    dev = torch.device("cuda:0")
+    cfg = config(args.config)
+    sets, start, n, cap = build_sets(cfg, args.sets, dev)
+    B, H, KVH = cfg["B"], cfg["H"], cfg["KVH"]
+    lib = _lib.load()
+    nbytes = int(lib.lcl_decode_workspace_bytes(B, H, n, qkv.BLOCK))
+    ws = torch.empty(nbytes // 4 + 1, dtype=torch.float32, device=dev)
+    outs = [torch.empty((B, H, 1, 128), dtype=torch.float16, device=dev) for _ in sets]
+    stream = _lib.stream_of(dev)
+    scale = 1 / np.sqrt(128)
+    K_ = args.steps
+    ev = Events(2 * K_ + 2)
+
+    def step(i, e0=None, e1=None):
+        q, K, V = sets[i % len(sets)]
+        rc = lib.lcl_qkv_attend_ex(_lib.ptr(q), 0, _lib.ptr(K[0]), _lib.ptr(K[1]), _lib.ptr(K[2]), _lib.ptr(V[0]),
+                                   _lib.ptr(V[1]), _lib.ptr(V[2]), 0, _lib.ptr(start), None, float(scale), B, H, KVH,
+                                   128, cap, n, qkv.BLOCK, _lib.ptr(outs[i % len(sets)]), _lib.ptr(ws), nbytes,
+                                   stream, e0, e1)
+        _lib.check(rc, "lcl_qkv_attend_ex")
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    # timed region: K steps; the pass-1 dispatch of each records its own start/stop events
+    t0 = time.perf_counter()
+    hip = ev.hip
+    hip.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+    hip.hipEventRecord(ev.ev[-2], stream)
+    for i in range(K_):
+        step(i, ev.ev[2 * i], ev.ev[2 * i + 1])
+    hip.hipEventRecord(ev.ev[-1], stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    region_ms = ev.ms(2 * K_, 2 * K_ + 1)
+    p1 = np.array([ev.ms(2 * i, 2 * i + 1) for i in range(K_)])
+    ev.close()
+
+    ms_step = region_ms / K_
+    b_step, b_p1 = step_bytes(cfg)
+    value = b_step / (ms_step * 1e-3) / 1e9
+    p1_us = float(p1.mean() * 1e3)
+    achieved = b_p1 / (p1.mean() * 1e-3) / 1e9
+    line = {
+        "metric": "decode-attn µs/step + HBM GB/s (% peak), B=16 8-bit KV GQA 32/8 D=128",
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": K_,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 5),
+        "us_per_step": round(ms_step * 1e3, 2),
+        "hbm_frac": round(value / HBM_PEAK_GBS, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "u8",
+        "data": "synthetic",
+        "config": {"workload": cfg["workload"], "B": B, "H": H, "KVH": KVH, "head_dim": 128,
+                   "contexts": [int(x) for x in cfg["nb"]], "sum_n": int(cfg["nb"].sum()), "cap": cap,
+                   "bytes_per_step": b_step, "buffer_sets": len(sets), "kv": "MLX affine 8-bit, group 64",
+                   "compute": "u8 codes -> fp16 MFMA (exact), fp32 accumulate", "block": qkv.BLOCK or "auto",
+                   "wall_s_timed": round(wall, 4)},
+        "roofline": {"bound": "hbm", "kernel": "qkv_pass1_q8", "achieved": round(achieved, 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "avg_us": round(p1_us, 2), "p10_us": round(float(np.percentile(p1, 10)) * 1e3, 2),
+                     "p90_us": round(float(np.percentile(p1, 90)) * 1e3, 2), "bytes_per_launch": b_p1,
+                     "traffic": _traffic(cfg["name"])},
+        "cpu_baseline": None,
+    }
+    if not args.no_cpu:
+        per, reps, threads, cpu, err = cpu_baseline(cfg, sets, start, n, args.cpu_seconds, outs[0])
+        line["cpu_baseline"] = {"value": round(b_step / per / 1e9, 3), "unit": "GB/s", "cores": threads,
+                                "kind": "port", "us_per_step": round(per * 1e6, 1), "cpu": cpu,
+                                "sample": f"{reps} whole steps of buffer set 0 (the same inputs as the GPU), "
+                                          f"C restatement of qkv.py's two passes (oracle/c/oracle.c), OpenMP",
+                                "max_abs_diff_vs_gpu": err}
+    print(json.dumps(line), flush=True)
+
+
+def _traffic(name):
+    """HBM bytes a pass-1 launch moved, from the committed rocprofv3 --pmc summary, or None."""
+    path = os.path.join(ROOT, "profiles", f"decode_q8_{name}_traffic.json")
+    try:
+        with open(path) as f:
+            return json.load(f).get("traffic_bytes_per_launch")
+    except (OSError, ValueError):
+        return None
+
+
+if __name__ == "__main__":
+    main()

@@ -40,12 +40,21 @@ size_t lcl_decode_workspace_bytes(int R, int H, int extent, int block);
  *   start  (B,) int32: row b attends to keys [max(start[b], 0), n); may be NULL (0)
  *   sinks  (H,) float32 logits in the softmax denominator only; may be NULL
  *   out    (B, H, 128) dtype qdt
- * cap must be a multiple of 16 and n <= cap.  `block` plays the role of the
+ * n <= cap (any capacity).  `block` plays the role of the
  * reference's BLOCK (locals/qkv.py:28): keys per pass-1 workgroup. */
 int lcl_qkv_attend(const void* q, int qdt, const uint32_t* kw, const void* ks, const void* kb, const uint32_t* vw,
                    const void* vs, const void* vb, int sdt, const int32_t* start, const float* sinks, float scale,
                    int B, int H, int KVH, int head_dim, int cap, int n, int block, void* out, void* workspace,
                    size_t workspace_bytes, void* stream);
+
+/* Profiling form of lcl_qkv_attend: the same call, with the pass-1 kernel's
+ * dispatch bracketed by two hipEvent_t (ev_start, ev_stop; either may be NULL)
+ * recorded by the dispatch itself.  No counterpart in the reference (it is for
+ * callers that time the dominant kernel, e.g. bench.py). */
+int lcl_qkv_attend_ex(const void* q, int qdt, const uint32_t* kw, const void* ks, const void* kb, const uint32_t* vw,
+                      const void* vs, const void* vb, int sdt, const int32_t* start, const float* sinks, float scale,
+                      int B, int H, int KVH, int head_dim, int cap, int n, int block, void* out, void* workspace,
+                      size_t workspace_bytes, void* stream, void* ev_start, void* ev_stop);
 
 /* attention.ragged_attention (locals/attention.py:200-224): row r of a packed
  * batch reads KV slot slots[r] and its first nkeys[r] keys.
@@ -57,6 +66,25 @@ int lcl_qkv_attend(const void* q, int qdt, const uint32_t* kw, const void* ks, c
 int lcl_ragged_attention(const void* q, int qdt, const void* keys, const void* values, int kvdt, const int32_t* slots,
                          const int32_t* nkeys, float scale, const float* scale_dev, int R, int H, int n_slots, int Hkv, int head_dim, int cap,
                          int block, void* out, void* workspace, size_t workspace_bytes, void* stream);
+
+/* BatchQuantizedKVCache.update_and_fetch's store (locals/qkv.py:309-326): MLX
+ * affine 8-bit quantization (mx.quantize, group 64, bits 8, called at
+ * locals/qkv.py:322-323) of a step's new keys k and values v, each
+ * (B, KVH, L, D) of dtype dt (f16 or bf16), written at positions
+ * [prev, prev + L) of the cache triples (B, KVH, cap, D/4) words and
+ * (B, KVH, cap, D/64) scales/biases of dtype dt.  v (and its triple) may be NULL.
+ * round_mode: 0 = ties away from zero (MLX's Metal path), 1 = ties to even
+ * (MLX's CPU path).  With cap == L and prev == 0 this is plain mx.quantize.
+ * Bit-exact: IEEE fp32 with correctly rounded division, RNE casts. */
+int lcl_quantize_append(const void* k, const void* v, int dt, uint32_t* kw, void* ks, void* kb, uint32_t* vw,
+                        void* vs, void* vb, int B, int KVH, int L, int D, int cap, int prev, int round_mode,
+                        void* stream);
+
+/* qkv.dequantized (locals/qkv.py:252-253, mx.dequantize): rows of D values
+ * scale * code + bias from (rows, D/4) words and (rows, D/64) scales/biases of
+ * dtype sdt, written as dtype odt (f16, bf16 or f32). */
+int lcl_dequantize(const uint32_t* words, const void* scales, const void* biases, int sdt, long long rows, int D,
+                   void* out, int odt, void* stream);
 
 #ifdef __cplusplus
 }

@@ -28,7 +28,10 @@ Z = ctypes.c_size_t
 SIGNATURES = {
     "lcl_decode_workspace_bytes": (Z, [I, I, I, I]),
     "lcl_qkv_attend": (I, [P, I, P, P, P, P, P, P, I, P, P, F, I, I, I, I, I, I, I, P, P, Z, P]),
+    "lcl_qkv_attend_ex": (I, [P, I, P, P, P, P, P, P, I, P, P, F, I, I, I, I, I, I, I, P, P, Z, P, P, P]),
     "lcl_ragged_attention": (I, [P, I, P, P, I, P, P, F, P, I, I, I, I, I, I, I, P, P, Z, P]),
+    "lcl_quantize_append": (I, [P, P, I, P, P, P, P, P, P, I, I, I, I, I, I, I, P]),
+    "lcl_dequantize": (I, [P, P, P, I, ctypes.c_longlong, I, P, I, P]),
 }
 
 _lib = None

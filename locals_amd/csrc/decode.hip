@@ -31,6 +31,8 @@
 // loads of V codes (4 keys x 2 groups) and 4 x 128-bit loads of the four keys'
 // scale/bias pairs; the next tile's loads are in flight while a tile computes.
 
+#include <hip/hip_ext.h>
+
 #include "lcl_common.h"
 #include "locals_amd.h"
 
@@ -141,18 +143,39 @@ __global__ __launch_bounds__(256) void qkv_pass1_q8(DecodeParams p) {
     // tile loads: K codes of key (tb + c16), the scale/bias quads and V codes of keys tb + 4q4 + k
     auto load_tile = [&](int tb, uint4& ka, uint4& kc, uint4& ksc, uint4& kbi, uint4& vsc, uint4& vbi,
                          uint32_t (&vd)[8]) {
-      const uint32_t* krow = p.kw + (tok0 + tb + c16) * 32;
-      ka = *reinterpret_cast<const uint4*>(krow + 4 * q4);
-      kc = *reinterpret_cast<const uint4*>(krow + 16 + 4 * q4);
-      const size_t ts = tok0 + tb + 4 * q4;
-      ksc = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(p.ks) + ts * 2);
-      kbi = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(p.kb) + ts * 2);
-      vsc = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(p.vs) + ts * 2);
-      vbi = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(p.vb) + ts * 2);
+      if (tb + 16 <= p.cap) {
+        const uint32_t* krow = p.kw + (tok0 + tb + c16) * 32;
+        ka = *reinterpret_cast<const uint4*>(krow + 4 * q4);
+        kc = *reinterpret_cast<const uint4*>(krow + 16 + 4 * q4);
+        const size_t ts = tok0 + tb + 4 * q4;
+        ksc = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(p.ks) + ts * 2);
+        kbi = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(p.kb) + ts * 2);
+        vsc = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(p.vs) + ts * 2);
+        vbi = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(p.vb) + ts * 2);
 #pragma unroll
-      for (int k = 0; k < 4; k++) {
-        vd[2 * k] = p.vw[(ts + k) * 32 + c16];
-        vd[2 * k + 1] = p.vw[(ts + k) * 32 + 16 + c16];
+        for (int k = 0; k < 4; k++) {
+          vd[2 * k] = p.vw[(ts + k) * 32 + c16];
+          vd[2 * k + 1] = p.vw[(ts + k) * 32 + 16 + c16];
+        }
+      } else {  // the tile runs past the buffer's capacity: clamp each key (those keys are masked)
+        const uint32_t* krow = p.kw + (tok0 + min(tb + c16, p.cap - 1)) * 32;
+        ka = *reinterpret_cast<const uint4*>(krow + 4 * q4);
+        kc = *reinterpret_cast<const uint4*>(krow + 16 + 4 * q4);
+        uint32_t e[4][4];
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+          const size_t tt = tok0 + min(tb + 4 * q4 + k, p.cap - 1);
+          e[0][k] = static_cast<const uint32_t*>(p.ks)[tt];
+          e[1][k] = static_cast<const uint32_t*>(p.kb)[tt];
+          e[2][k] = static_cast<const uint32_t*>(p.vs)[tt];
+          e[3][k] = static_cast<const uint32_t*>(p.vb)[tt];
+          vd[2 * k] = p.vw[tt * 32 + c16];
+          vd[2 * k + 1] = p.vw[tt * 32 + 16 + c16];
+        }
+        ksc = make_uint4(e[0][0], e[0][1], e[0][2], e[0][3]);
+        kbi = make_uint4(e[1][0], e[1][1], e[1][2], e[1][3]);
+        vsc = make_uint4(e[2][0], e[2][1], e[2][2], e[2][3]);
+        vbi = make_uint4(e[3][0], e[3][1], e[3][2], e[3][3]);
       }
     };
     uint4 ka, kc, ksc, kbi, vsc, vbi;
@@ -342,11 +365,13 @@ __global__ __launch_bounds__(256) void ragged_pass1_16(DecodeParams p) {
   if (tlo < thi) {
     const int tb0 = tlo & ~15;
     auto load_tile = [&](int tb, uint4 (&kd)[4], uint4 (&vd)[4]) {
-      const uint16_t* krow = K + (tok0 + tb + c16) * kHD + 32 * q4;
+      const int last = p.cap - 1;  // keys past the capacity (only in a row's last tile) are clamped and masked
+      const uint16_t* krow = K + (tok0 + min(tb + c16, last)) * kHD + 32 * q4;
 #pragma unroll
       for (int u = 0; u < 4; u++) kd[u] = *reinterpret_cast<const uint4*>(krow + 8 * u);
 #pragma unroll
-      for (int k = 0; k < 4; k++) vd[k] = *reinterpret_cast<const uint4*>(V + (tok0 + tb + 4 * q4 + k) * kHD + 8 * c16);
+      for (int k = 0; k < 4; k++)
+        vd[k] = *reinterpret_cast<const uint4*>(V + (tok0 + min(tb + 4 * q4 + k, last)) * kHD + 8 * c16);
     };
     uint4 kd[4], vd[4];
     load_tile(tb0, kd, vd);
@@ -545,10 +570,18 @@ int lcl_qkv_attend(const void* q, int qdt, const uint32_t* kw, const void* ks, c
                    const void* vs, const void* vb, int sdt, const int32_t* start, const float* sinks, float scale,
                    int B, int H, int KVH, int hd, int cap, int n, int block, void* out, void* workspace,
                    size_t workspace_bytes, void* stream_) {
+  return lcl_qkv_attend_ex(q, qdt, kw, ks, kb, vw, vs, vb, sdt, start, sinks, scale, B, H, KVH, hd, cap, n, block,
+                           out, workspace, workspace_bytes, stream_, nullptr, nullptr);
+}
+
+int lcl_qkv_attend_ex(const void* q, int qdt, const uint32_t* kw, const void* ks, const void* kb, const uint32_t* vw,
+                      const void* vs, const void* vb, int sdt, const int32_t* start, const float* sinks, float scale,
+                      int B, int H, int KVH, int hd, int cap, int n, int block, void* out, void* workspace,
+                      size_t workspace_bytes, void* stream_, void* ev_start, void* ev_stop) {
   hipStream_t stream = static_cast<hipStream_t>(stream_);
   if (!q || !kw || !ks || !kb || !vw || !vs || !vb || !out) return -1;
   if (hd != kHD) return -2;
-  if (B <= 0 || H <= 0 || KVH <= 0 || H % KVH || cap <= 0 || cap % 16 || n < 0 || n > cap) return -1;
+  if (B <= 0 || H <= 0 || KVH <= 0 || H % KVH || cap <= 0 || n < 0 || n > cap) return -1;
   if (block < 0 || block % 64) return -1;
   if ((qdt != DT_F16 && qdt != DT_BF16 && qdt != DT_F32) || (sdt != DT_F16 && sdt != DT_BF16)) return -1;
   const int chunk = pick_chunk(block, n);
@@ -571,8 +604,9 @@ int lcl_qkv_attend(const void* q, int qdt, const uint32_t* kw, const void* ks, c
   p.qdt = qdt; p.sdt = sdt;
   if (n > 0) {
     const dim3 grid(nchunks, KVH * p.nslices, B);
-    if (sdt == DT_BF16) hipLaunchKernelGGL(qkv_pass1_q8<DT_BF16>, grid, dim3(256), 0, stream, p);
-    else hipLaunchKernelGGL(qkv_pass1_q8<DT_F16>, grid, dim3(256), 0, stream, p);
+    hipEvent_t e0 = static_cast<hipEvent_t>(ev_start), e1 = static_cast<hipEvent_t>(ev_stop);
+    if (sdt == DT_BF16) hipExtLaunchKernelGGL(qkv_pass1_q8<DT_BF16>, grid, dim3(256), 0, stream, e0, e1, 0, p);
+    else hipExtLaunchKernelGGL(qkv_pass1_q8<DT_F16>, grid, dim3(256), 0, stream, e0, e1, 0, p);
   }
   CombineParams c{};
   c.pm = p.pm; c.pl = p.pl; c.po = p.po; c.sinks = sinks; c.out = out;
@@ -587,7 +621,7 @@ int lcl_ragged_attention(const void* q, int qdt, const void* keys, const void* v
   hipStream_t stream = static_cast<hipStream_t>(stream_);
   if (!q || !keys || !values || !slots || !nkeys || !out) return -1;
   if (hd != kHD) return -2;
-  if (R < 0 || H <= 0 || Hkv <= 0 || H % Hkv || n_slots <= 0 || cap <= 0 || cap % 16) return -1;
+  if (R < 0 || H <= 0 || Hkv <= 0 || H % Hkv || n_slots <= 0 || cap <= 0) return -1;
   if (block < 0 || block % 64) return -1;
   if ((qdt != DT_F16 && qdt != DT_BF16 && qdt != DT_F32) || (kvdt != DT_F16 && kvdt != DT_BF16)) return -1;
   if (R == 0) return 0;

@@ -1,0 +1,157 @@
+// MLX affine 8-bit quantization (group 64) and its cache append, bit-exact.
+//
+// Reference behaviour: BatchQuantizedKVCache.update_and_fetch (locals/qkv.py:309-326)
+// quantizes the step's new keys and values with mx.quantize(x, group_size=64, bits=8)
+// and writes the (words, scales, biases) triples at positions [prev, prev + L) of the
+// cache buffers (B, KVH, cap, .); dequantized (locals/qkv.py:252-253) is
+// mx.dequantize.  Per group of 64 values (fp32 arithmetic, correctly rounded division):
+//     scale = max((max - min) / 255, 1e-7); side = |min| > |max|; scale = side ? scale : -scale
+//     edge = side ? min : max; q0 = round(edge / scale)
+//     q0 != 0: scale = edge / q0, bias = edge;  else bias = 0
+//     code = clamp(round((w - bias) / scale), 0, 255); scale, bias stored in the input dtype (RNE)
+// round() ties away from zero (MLX's Metal path) or to even (MLX's CPU path), by argument.
+//
+// MI355X mapping: one wave quantizes four 64-value groups; a lane owns 4 values
+// (one output word, 8-byte load), group min/max by a 4-step xor reduction over its
+// 16 lanes, one 32-bit store per lane and one scale/bias store per group.  K and V
+// of a step share one launch (blockIdx.y).  HBM-bound: 2 B read + 1.06 B written a
+// value.  Dequantization is the mirror image (one word in, 4 values out a lane).
+
+#include "lcl_common.h"
+#include "locals_amd.h"
+
+namespace lcl {
+
+struct QuantParams {
+  const void* src[2];  // (B, KVH, L, D) rows, dtype dt; src[1] may be null
+  uint32_t* words[2];  // (B, KVH, cap, D/4)
+  void* scales[2];     // (B, KVH, cap, D/64), dtype dt
+  void* biases[2];
+  long long rows;      // B * KVH * L
+  int L, D, cap, prev, dt, round_even;
+};
+
+__device__ __forceinline__ float round_mode(float x, int even) { return even ? __builtin_rintf(x) : __builtin_roundf(x); }
+
+__global__ __launch_bounds__(256) void quantize_append(QuantParams p) {
+  const int which = blockIdx.y;
+  if (!p.src[which]) return;
+  const int lane = threadIdx.x & 63;
+  const int groups_per_row = p.D / 64;
+  const long long gid = (static_cast<long long>(blockIdx.x) * 256 + threadIdx.x) / 16;  // global group index
+  const long long ngroups = p.rows * groups_per_row;
+  if (gid >= ngroups) return;  // whole 16-lane groups exit together
+  const long long row = gid / groups_per_row;
+  const int g = int(gid % groups_per_row);
+  const int sub = lane & 15;  // lane within the group: values 4 sub .. 4 sub + 3
+  const uint16_t* src = static_cast<const uint16_t*>(p.src[which]);
+  const uint2 raw = *reinterpret_cast<const uint2*>(src + row * p.D + g * 64 + 4 * sub);
+  float w[4];
+  w[0] = half_of(raw.x, 0, p.dt);
+  w[1] = half_of(raw.x, 1, p.dt);
+  w[2] = half_of(raw.y, 0, p.dt);
+  w[3] = half_of(raw.y, 1, p.dt);
+  float mx = fmaxf(fmaxf(w[0], w[1]), fmaxf(w[2], w[3]));
+  float mn = fminf(fminf(w[0], w[1]), fminf(w[2], w[3]));
+#pragma unroll
+  for (int m = 1; m < 16; m <<= 1) {
+    mx = fmaxf(mx, __shfl_xor(mx, m));
+    mn = fminf(mn, __shfl_xor(mn, m));
+  }
+  const float n_bins = 255.0f, eps = 1e-7f;
+  float scale = fmaxf((mx - mn) / n_bins, eps);
+  const bool side = fabsf(mn) > fabsf(mx);
+  scale = side ? scale : -scale;
+  const float edge = side ? mn : mx;
+  const float q0 = round_mode(edge / scale, p.round_even);
+  float bias = 0.0f;
+  if (q0 != 0.0f) {
+    scale = edge / q0;
+    bias = edge;
+  }
+  uint32_t word = 0;
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    float c = round_mode((w[i] - bias) / scale, p.round_even);
+    c = fminf(fmaxf(c, 0.0f), n_bins);
+    word |= uint32_t(c) << (8 * i);
+  }
+  // destination row: (b, h, prev + l) of the (B, KVH, cap, .) buffers
+  const long long bh = row / p.L;
+  const int l = int(row % p.L);
+  const long long drow = bh * p.cap + p.prev + l;
+  p.words[which][drow * (p.D / 4) + g * 16 + sub] = word;
+  if (sub == 0) {
+    store_from_f32(p.scales[which], drow * groups_per_row + g, scale, p.dt);
+    store_from_f32(p.biases[which], drow * groups_per_row + g, bias, p.dt);
+  }
+}
+
+struct DequantParams {
+  const uint32_t* words;
+  const void* scales;
+  const void* biases;
+  void* out;
+  long long rows;  // rows of D values (words rows)
+  int D, sdt, odt;
+};
+
+__global__ __launch_bounds__(256) void dequantize_rows(DequantParams p) {
+  const long long wid = static_cast<long long>(blockIdx.x) * 256 + threadIdx.x;  // word index
+  const int wpr = p.D / 4;
+  if (wid >= p.rows * wpr) return;
+  const long long row = wid / wpr;
+  const int w = int(wid % wpr);
+  const int g = w / 16;
+  const uint32_t x = p.words[wid];
+  const float s = load_as_f32(p.scales, row * (p.D / 64) + g, p.sdt);
+  const float b = load_as_f32(p.biases, row * (p.D / 64) + g, p.sdt);
+#pragma unroll
+  for (int i = 0; i < 4; i++) store_from_f32(p.out, row * p.D + 4 * w + i, s * float((x >> (8 * i)) & 0xffu) + b, p.odt);
+}
+
+}  // namespace lcl
+
+using namespace lcl;
+
+extern "C" {
+
+int lcl_quantize_append(const void* k, const void* v, int dt, uint32_t* kw, void* ks, void* kb, uint32_t* vw,
+                        void* vs, void* vb, int B, int KVH, int L, int D, int cap, int prev, int round_mode,
+                        void* stream_) {
+  hipStream_t stream = static_cast<hipStream_t>(stream_);
+  if (!k || !kw || !ks || !kb) return -1;
+  if (v && (!vw || !vs || !vb)) return -1;
+  if (dt != DT_F16 && dt != DT_BF16) return -1;
+  if (B < 0 || KVH <= 0 || L < 0 || D <= 0 || D % 64 || cap <= 0 || prev < 0 || prev + L > cap) return -1;
+  if (round_mode != 0 && round_mode != 1) return -1;
+  if (B == 0 || L == 0) return 0;
+  QuantParams p{};
+  p.src[0] = k; p.src[1] = v;
+  p.words[0] = kw; p.words[1] = vw;
+  p.scales[0] = ks; p.scales[1] = vs;
+  p.biases[0] = kb; p.biases[1] = vb;
+  p.rows = static_cast<long long>(B) * KVH * L;
+  p.L = L; p.D = D; p.cap = cap; p.prev = prev; p.dt = dt; p.round_even = round_mode;
+  const long long groups = p.rows * (D / 64);
+  const long long blocks = (groups * 16 + 255) / 256;
+  if (blocks > 0x7fffffffLL) return -2;
+  hipLaunchKernelGGL(quantize_append, dim3(unsigned(blocks), 2), dim3(256), 0, stream, p);
+  return int(hipGetLastError());
+}
+
+int lcl_dequantize(const uint32_t* words, const void* scales, const void* biases, int sdt, long long rows, int D,
+                   void* out, int odt, void* stream_) {
+  hipStream_t stream = static_cast<hipStream_t>(stream_);
+  if (!words || !scales || !biases || !out) return -1;
+  if (rows < 0 || D <= 0 || D % 64) return -1;
+  if ((sdt != DT_F16 && sdt != DT_BF16) || (odt != DT_F16 && odt != DT_BF16 && odt != DT_F32)) return -1;
+  if (rows == 0) return 0;
+  DequantParams p{words, scales, biases, out, rows, D, sdt, odt};
+  const long long blocks = (rows * (D / 4) + 255) / 256;
+  if (blocks > 0x7fffffffLL) return -2;
+  hipLaunchKernelGGL(dequantize_rows, dim3(unsigned(blocks)), dim3(256), 0, stream, p);
+  return int(hipGetLastError());
+}
+
+}  // extern "C"

@@ -102,3 +102,399 @@ def attend(q: torch.Tensor, keys, values, n: int, sinks: Optional[torch.Tensor],
                             nbytes, _lib.stream_of(dev))
     _lib.check(rc, "lcl_qkv_attend")
     return out
+
+
+ROUND_MODE = os.environ.get("LOCALS_AMD_ROUND", "away")  # "away": MLX's Metal mx.quantize; "even": its CPU path
+
+
+def _round_code(mode: Optional[str] = None) -> int:
+    m = ROUND_MODE if mode is None else mode
+    if m not in ("away", "even"):
+        raise ValueError("round mode must be 'away' or 'even'")
+    return 0 if m == "away" else 1
+
+
+def quantize_into(keys: torch.Tensor, values: Optional[torch.Tensor], kbuf, vbuf, prev: int,
+                  round_mode: Optional[str] = None) -> None:
+    """Quantize (B, KVH, L, D) ``keys`` (and ``values``) with MLX's affine 8 bits (group 64) into positions
+    [prev, prev + L) of the (B, KVH, cap, .) triples ``kbuf``/``vbuf`` (locals/qkv.py:320-325), one launch."""
+    if keys.dim() != 4:
+        raise ValueError("keys must be (B, KVH, L, D)")
+    B, KVH, L, D = keys.shape
+    if keys.dtype not in (torch.float16, torch.bfloat16):
+        raise ValueError("8-bit caches take float16 or bfloat16 keys and values")
+    _check_triple(kbuf, "key buffers")
+    cap = kbuf[0].shape[2]
+    if kbuf[0].shape[:2] != (B, KVH) or kbuf[0].shape[3] * 4 != D or kbuf[1].dtype != keys.dtype:
+        raise ValueError("key buffers do not match the keys")
+    if values is not None:
+        _check_triple(vbuf, "value buffers")
+        if values.shape != keys.shape or values.dtype != keys.dtype or vbuf[0].shape != kbuf[0].shape:
+            raise ValueError("values must match keys")
+    if not 0 <= prev <= cap - L:
+        raise ValueError("write past the buffers' capacity")
+    dev = _lib.require_gpu(keys, values, *kbuf, *(vbuf or ()))
+    keys = keys.contiguous()
+    values = values.contiguous() if values is not None else None
+    v3 = vbuf if values is not None else (None, None, None)
+    rc = _lib.load().lcl_quantize_append(
+        _lib.ptr(keys), _lib.ptr(values), _lib.dtype_code(keys.dtype), _lib.ptr(kbuf[0]), _lib.ptr(kbuf[1]),
+        _lib.ptr(kbuf[2]), _lib.ptr(v3[0]), _lib.ptr(v3[1]), _lib.ptr(v3[2]), B, KVH, L, D, cap, prev,
+        _round_code(round_mode), _lib.stream_of(dev))
+    _lib.check(rc, "lcl_quantize_append")
+
+
+def quantize(x: torch.Tensor, group_size: int = GROUP, bits: int = BITS, round_mode: Optional[str] = None):
+    """``mx.quantize(x, group_size=64, bits=8)`` (affine) of a 16-bit (..., D) tensor: (words int32 (..., D/4),
+    scales (..., D/64), biases (..., D/64)), bit-exact with MLX's closed form."""
+    if group_size != GROUP or bits != BITS:
+        raise ValueError("only group_size=64, bits=8 (the reference's 8-bit KV)")
+    shape = x.shape
+    D = shape[-1]
+    x4 = x.reshape(1, 1, -1, D)
+    out = _zeros_like_shape(1, 1, x4.shape[2], D, x.dtype, x.device, empty=True)
+    quantize_into(x4, None, out, None, 0, round_mode)
+    return tuple(a.reshape(*shape[:-1], a.shape[-1]) for a in out)
+
+
+def dequantized(t, dtype: Optional[torch.dtype] = None) -> torch.Tensor:
+    """``mx.dequantize(*t, group_size=64, bits=8)`` (locals/qkv.py:252-253): scale * code + bias in the scales'
+    dtype (or ``dtype``)."""
+    w, s, b = t
+    if not _words_ok(w) or s.dtype not in (torch.float16, torch.bfloat16) or b.dtype != s.dtype:
+        raise ValueError("dequantized takes an 8-bit (words, scales, biases) triple")
+    D = w.shape[-1] * 4
+    odt = dtype or s.dtype
+    dev = _lib.require_gpu(w, s, b)
+    w, s, b = w.contiguous(), s.contiguous(), b.contiguous()
+    out = torch.empty(*w.shape[:-1], D, dtype=odt, device=dev)
+    rows = w.numel() // w.shape[-1] if w.numel() else 0
+    rc = _lib.load().lcl_dequantize(_lib.ptr(w), _lib.ptr(s), _lib.ptr(b), _lib.dtype_code(s.dtype), rows, D,
+                                    _lib.ptr(out), _lib.dtype_code(odt), _lib.stream_of(dev))
+    _lib.check(rc, "lcl_dequantize")
+    return out
+
+
+def quantized(cache) -> bool:
+    """Whether ``cache`` keeps 8-bit keys and values (locals/qkv.py:256-257)."""
+    return getattr(cache, "bits", None) == BITS and getattr(cache, "group_size", None) == GROUP
+
+
+def attention(q, k, v, cache, scale: float, mask, sinks) -> torch.Tensor:
+    """A layer's attention through a quantized cache (locals/qkv.py:260-272): stores ``k``/``v`` (B, KVH, L, HD),
+    then one query a row through ``attend``, a prompt or a tree (several) through the masked 8-bit kernel."""
+    keys, values = cache.update_and_fetch(k, v)
+    if q.shape[2] == 1 and q.shape[3] == 128:
+        start = getattr(cache, "left_padding", None)
+        if start is None:
+            start = torch.zeros((q.shape[0],), dtype=torch.int32, device=q.device)
+        n = cache._idx if hasattr(cache, "_idx") else cache.offset
+        return attend(q, cache.keys, cache.values, n, sinks, scale, start)
+    from .fuse import attend_few_q8
+
+    return attend_few_q8(q, keys, values, scale, mask, sinks)
+
+
+def _zeros_like_shape(B, H, n, D, dtype, device, empty=False):
+    mk = torch.empty if empty else torch.zeros
+    return (mk((B, H, n, D * BITS // 32), dtype=torch.int32, device=device),
+            mk((B, H, n, D // GROUP), dtype=dtype, device=device),
+            mk((B, H, n, D // GROUP), dtype=dtype, device=device))
+
+
+def _zeros(B, H, n, D, dtype, device=None):
+    """Empty 8-bit buffers (locals/qkv.py:275-277)."""
+    return _zeros_like_shape(B, H, n, D, dtype, device)
+
+
+def _head_dim(t):
+    return t[0].shape[-1] * 32 // BITS
+
+
+def _slice(t, lo=None, hi=None):
+    return tuple(a[..., lo:hi, :] for a in t)
+
+
+def create_causal_mask(N: int, offset: int = 0, window_size: Optional[int] = None, right_padding=None,
+                       left_padding=None, device=None) -> torch.Tensor:
+    """mlx-lm's ``create_causal_mask`` as BatchQuantizedKVCache.make_mask uses it (locals/qkv.py:367-368):
+    (N, offset + N) bool, or (B, 1, N, offset + N) with per-row padding."""
+    rinds = torch.arange(offset + N, device=device)
+    linds = torch.arange(offset, offset + N, device=device)[:, None]
+    mask = linds >= rinds[None]
+    if window_size is not None:
+        mask = mask & (linds < rinds[None] + window_size)
+    if right_padding is not None:
+        rp = torch.as_tensor(right_padding, device=device).reshape(-1, 1, 1, 1)
+        mask = mask & (rinds < (offset + N) - rp)
+    if left_padding is not None:
+        lp = torch.as_tensor(left_padding, device=device).reshape(-1, 1, 1, 1)
+        mask = mask & (lp <= rinds)
+    return mask
+
+
+def dynamic_roll(a: torch.Tensor, shifts: torch.Tensor, axis: int = 2) -> torch.Tensor:
+    """mlx-lm's ``dynamic_roll`` along ``axis`` with one shift a row (row = dim 0), used by ``finalize``."""
+    n = a.shape[axis]
+    idx = (torch.arange(n, device=a.device)[None, :] - shifts.reshape(-1, 1).to(a.device)) % n  # (B, n)
+    shape = [a.shape[0]] + [1] * (a.dim() - 1)
+    shape[axis] = n
+    idx = idx.reshape(shape).expand_as(a)
+    return torch.gather(a, axis, idx)
+
+
+class QuantizedKVCache8:
+    """mlx-lm's QuantizedKVCache in 8 bits (locals/qkv.py:284-292): one request's (words, scales, biases) buffers
+    growing by ``step`` positions; ``merge`` makes a BatchQuantizedKVCache."""
+
+    step = 256
+    bits, group_size = BITS, GROUP
+
+    def __init__(self):
+        self.keys = self.values = None
+        self.offset = 0
+
+    def update_and_fetch(self, keys: torch.Tensor, values: torch.Tensor):
+        B, H, S, D = keys.shape
+        prev = self.offset
+        if self.keys is None or prev + S > self.keys[0].shape[2]:
+            cap = (prev + S + self.step - 1) // self.step * self.step
+            nk = _zeros(B, H, cap, D, keys.dtype, keys.device)
+            nv = _zeros(B, H, cap, values.shape[3], values.dtype, values.device)
+            if self.keys is not None:
+                for a, z in zip(self.keys + self.values, nk + nv):
+                    z[..., :prev, :] = a[..., :prev, :]
+            self.keys, self.values = nk, nv
+        quantize_into(keys, values, self.keys, self.values, prev)
+        self.offset += S
+        return _slice(self.keys, None, self.offset), _slice(self.values, None, self.offset)
+
+    @property
+    def state(self):
+        if self.keys is None:
+            return self.keys, self.values
+        return _slice(self.keys, None, self.offset), _slice(self.values, None, self.offset)
+
+    @state.setter
+    def state(self, v):
+        self.keys, self.values = v
+        self.offset = self.keys[0].shape[2]
+
+    def is_trimmable(self):
+        return True
+
+    def trim(self, n):
+        n = min(self.offset, n)
+        self.offset -= n
+        return n
+
+    def make_mask(self, N: int, return_array: bool = False, window_size: Optional[int] = None, **kwargs):
+        if N == 1 and not return_array:
+            return None
+        if window_size is None and not return_array:
+            return "causal"
+        dev = self.keys[0].device if self.keys is not None else None
+        return create_causal_mask(N, offset=self.offset, window_size=window_size, device=dev)
+
+    def size(self):
+        return self.offset
+
+    def empty(self):
+        return self.keys is None
+
+    @property
+    def nbytes(self):
+        if self.keys is None:
+            return 0
+        return sum(a.numel() * a.element_size() for a in self.keys + self.values)
+
+    @classmethod
+    def merge(cls, caches):
+        return BatchQuantizedKVCache.merge(caches)
+
+
+class BatchQuantizedKVCache:
+    """mlx-lm's BatchKVCache (left-padded rows, one buffer index ``_idx``, ``offset`` each row's position) with the
+    keys and values as 8-bit (words, scales, biases) triples (locals/qkv.py:295-452).  ``left_padding`` and
+    ``offset`` are int32 device tensors; ``_idx`` is a host int.  Capacities grow by whole ``step``s."""
+
+    step = 256
+    bits, group_size = BITS, GROUP
+
+    def __init__(self, left_padding: List[int], device=None):
+        self.keys = self.values = None
+        self.left_padding = torch.as_tensor(left_padding, dtype=torch.int32, device=device)
+        self.offset = -self.left_padding.clone()
+        self._idx = 0
+        self._right_padding = None
+
+    def _dev(self):
+        return self.left_padding.device
+
+    def update_and_fetch(self, keys: torch.Tensor, values: torch.Tensor):
+        prev, S = self._idx, keys.shape[2]
+        if self.left_padding.device != keys.device:
+            self.left_padding = self.left_padding.to(keys.device)
+            self.offset = self.offset.to(keys.device)
+        if self.keys is None or prev + S > self.keys[0].shape[2]:
+            B, H, _, D = keys.shape
+            cap = (prev + S + self.step - 1) // self.step * self.step
+            nk = _zeros(B, H, cap, D, keys.dtype, keys.device)
+            nv = _zeros(B, H, cap, values.shape[3], values.dtype, values.device)
+            if self.keys is not None:
+                for a, z in zip(self.keys + self.values, nk + nv):
+                    z[..., :prev, :] = a[..., :prev, :]
+            self.keys, self.values = nk, nv
+        self.offset = self.offset + S
+        self._idx += S
+        quantize_into(keys, values, self.keys, self.values, prev)
+        return self.keys_and_values()
+
+    def keys_and_values(self):
+        return _slice(self.keys, None, self._idx), _slice(self.values, None, self._idx)
+
+    def prepare(self, *, left_padding=None, lengths=None, right_padding=None):
+        if left_padding is not None:
+            if self.keys is not None:
+                raise ValueError("left padding can only be added to an empty cache")
+            lp = torch.as_tensor(left_padding, dtype=torch.int32, device=self._dev())
+            self.left_padding = self.left_padding + lp
+            self.offset = self.offset - lp
+        if right_padding is not None and max(right_padding) > 0:
+            self._right_padding = torch.as_tensor(right_padding, dtype=torch.int32, device=self._dev())
+
+    def finalize(self):
+        if self._right_padding is not None:
+            p = self._right_padding
+            self.keys = tuple(dynamic_roll(a, p) for a in self.keys)
+            self.values = tuple(dynamic_roll(a, p) for a in self.values)
+            self.offset = self.offset - p
+            self.left_padding = self.left_padding + p
+            self._right_padding = None
+
+    @property
+    def state(self):
+        return self.keys, self.values, self.offset, self.left_padding, self._idx
+
+    @state.setter
+    def state(self, v):
+        self.keys, self.values, self.offset, self.left_padding, self._idx = v
+
+    def is_trimmable(self):
+        return True
+
+    def trim(self, n):
+        n = min(self._idx, n)
+        self._idx -= n
+        self.offset = self.offset - n
+        return n
+
+    def make_mask(self, N: int, return_array: bool = False, **kwargs):
+        return create_causal_mask(N, offset=self._idx, left_padding=self.left_padding, device=self._dev(), **kwargs)
+
+    def filter(self, batch_indices):
+        idx = torch.as_tensor(batch_indices, device=self._dev(), dtype=torch.long)
+        if self.keys is not None:
+            self.keys = tuple(a[idx] for a in self.keys)
+            self.values = tuple(a[idx] for a in self.values)
+        self.offset = self.offset[idx]
+        self.left_padding = self.left_padding[idx]
+        drop = int(self.left_padding.min().item()) if self.left_padding.numel() else 0
+        if drop > 0:
+            if self.keys is not None:
+                self.keys = tuple(a[..., drop:, :].contiguous() for a in self.keys)
+                self.values = tuple(a[..., drop:, :].contiguous() for a in self.values)
+            self._idx -= drop
+            self.left_padding = self.left_padding - drop
+
+    def extend(self, other):
+        if self.keys is None and other.keys is None:
+            self.left_padding = torch.cat([self.left_padding, other.left_padding.to(self._dev())])
+            self.offset = torch.cat([self.offset, other.offset.to(self._dev())])
+            return
+        ref = self if self.keys is not None else other
+        H, D, M, dtype = ref.keys[0].shape[1], _head_dim(ref.keys), _head_dim(ref.values), ref.keys[1].dtype
+        dev = ref.keys[0].device
+        max_idx = max(self._idx, other._idx)
+        size = max(c.keys[0].shape[2] for c in (self, other) if c.keys is not None)
+
+        def pad(c):
+            k = c.keys if c.keys is not None else _zeros(c.offset.shape[0], H, 0, D, dtype, dev)
+            v = c.values if c.values is not None else _zeros(c.offset.shape[0], H, 0, M, dtype, dev)
+            left = max_idx - c._idx
+            right = size - k[0].shape[2] - left
+            if right < 0:
+                k, v = _slice(k, None, right), _slice(v, None, right)
+                right = 0
+            if left or right:
+                k = tuple(torch.nn.functional.pad(a, (0, 0, left, right)) for a in k)
+                v = tuple(torch.nn.functional.pad(a, (0, 0, left, right)) for a in v)
+            return k, v, c.offset.to(dev), c.left_padding.to(dev) + left
+
+        (k1, v1, o1, p1), (k2, v2, o2, p2) = pad(self), pad(other)
+        self.keys = tuple(torch.cat([a, b]) for a, b in zip(k1, k2))
+        self.values = tuple(torch.cat([a, b]) for a, b in zip(v1, v2))
+        self.offset, self.left_padding = torch.cat([o1, o2]), torch.cat([p1, p2])
+        self._idx = max_idx
+
+    def extract(self, idx):
+        c = QuantizedKVCache8()
+        p = int(self.left_padding[idx].item())
+        c.keys = tuple(a[idx:idx + 1, :, p:self._idx].contiguous() for a in self.keys)
+        c.values = tuple(a[idx:idx + 1, :, p:self._idx].contiguous() for a in self.values)
+        c.offset = c.keys[0].shape[2]
+        return c
+
+    @classmethod
+    def merge(cls, caches):
+        lengths = [c.offset if c.keys is not None else 0 for c in caches]
+        L = max(lengths)
+        ref = next((c for c in caches if c.keys is not None), None)
+        dev = ref.keys[0].device if ref is not None else None
+        out = cls([L - n for n in lengths], device=dev)
+        if L == 0:
+            return out
+        H, D, M, dtype = ref.keys[0].shape[1], _head_dim(ref.keys), _head_dim(ref.values), ref.keys[1].dtype
+        keys, values = _zeros(len(caches), H, L, D, dtype, dev), _zeros(len(caches), H, L, M, dtype, dev)
+        for i, (n, c) in enumerate(zip(lengths, caches)):
+            if n:
+                for a, x in zip(keys, c.keys):
+                    a[i:i + 1, :, L - n:] = x[..., :n, :]
+                for a, x in zip(values, c.values):
+                    a[i:i + 1, :, L - n:] = x[..., :n, :]
+        out.keys, out.values, out._idx = keys, values, L
+        out.offset = out.offset + L
+        return out
+
+    def size(self):
+        return self._idx
+
+    def empty(self):
+        return self.keys is None
+
+    @property
+    def nbytes(self):
+        if self.keys is None:
+            return 0
+        return sum(a.numel() * a.element_size() for a in self.keys + self.values)
+
+
+def wants_8bit(model) -> bool:
+    """Whether full-attention layers keep 8-bit keys and values: LOCALS_KV_BITS=8 (locals/qkv.py:455-460)."""
+    return os.environ.get("LOCALS_KV_BITS", "16") == "8"
+
+
+def opt_in(model) -> Optional[bool]:
+    """Full-attention layers of a model in QuantizedKVCache8 (its make_cache replaced); True if done
+    (locals/qkv.py:463-472).  Sliding-window layers keep whatever cache ``model.make_cache`` made for them."""
+    if not wants_8bit(model):
+        return False
+    layers = model.layers
+    base = getattr(model, "make_cache", None)
+
+    def make_cache():
+        made = base() if base is not None else [None] * len(layers)
+        return [c if getattr(l, "use_sliding", False) else QuantizedKVCache8() for l, c in zip(layers, made)]
+
+    model.make_cache = make_cache
+    return True
