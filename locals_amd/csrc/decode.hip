@@ -82,19 +82,58 @@ __device__ __forceinline__ void row_range(const int32_t* start, const int32_t* n
   hi = nkeys ? min(max(nkeys[r], 0), cap) : n;
 }
 
-// Q^T as the B operand: lane (head c16, quad q4) holds q[head][dim(j, q4, i)], i = 0..3
-__device__ __forceinline__ void load_q_cols(const DecodeParams& p, size_t qrow, bool real, int dim0, _Float16 (&qh)[4],
-                                            float& qsum) {
+// Join the 4 waves' (m, l, o[128]) of each head of the slice into one part per
+// (row, head, chunk) of the split-K workspace.
+__device__ __forceinline__ void join_waves(const DecodeParams& p, const float (&s_m)[kWaves][16],
+                                           const float (&s_l)[kWaves][16], const float (&s_o)[kWaves][16][kHD],
+                                           int Gs, int r, int head0, int c) {
+  for (int e = threadIdx.x; e < Gs * kHD; e += 256) {
+    const int h = e >> 7, d = e & (kHD - 1);
+    float M = -INFINITY;
 #pragma unroll
-  for (int i = 0; i < 4; i++) {
-    const float v = real ? load_as_f32(p.q, qrow * kHD + dim0 + i, p.qdt) : 0.0f;
-    qh[i] = _Float16(v);
-    qsum += float(qh[i]);
+    for (int w = 0; w < kWaves; w++) M = fmaxf(M, s_m[w][h]);
+    float L = 0.0f, o = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kWaves; w++) {
+      const float f = s_m[w][h] == -INFINITY ? 0.0f : fast_exp2(s_m[w][h] - M);
+      L += f * s_l[w][h];
+      o += f * s_o[w][h][d];
+    }
+    const size_t part = (size_t(r) * p.H + head0 + h) * p.nchunks + c;
+    p.po[part * kHD + d] = o;
+    if (d == 0) {
+      p.pm[part] = M;
+      p.pl[part] = L;
+    }
   }
 }
 
+template <int DT>
+__device__ __forceinline__ float ld16(const void* p, size_t i) {
+  if constexpr (DT == DT_F32) return static_cast<const float*>(p)[i];
+  else if constexpr (DT == DT_BF16) return bf16_bits_to_f32(static_cast<const uint16_t*>(p)[i]);
+  else return f16_bits_to_f32(static_cast<const uint16_t*>(p)[i]);
+}
+
+template <int DT>
+__device__ __forceinline__ float hpart(uint32_t w, int k) {
+  const uint16_t b = uint16_t(k ? (w >> 16) : (w & 0xffffu));
+  return DT == DT_BF16 ? bf16_bits_to_f32(b) : f16_bits_to_f32(b);
+}
+
+// One 16-key tile of 8-bit K/V as a lane holds it:
+//  ka, kc  K codes of key (tb + c16), dims [16 q4, +16) and [64 + 16 q4, +16)
+//  sc[j][k] for keys tb + 4 q4 + k: j = 0 K scales, 1 K biases, 2 V scales, 3 V biases (a 16-bit pair a key)
+//  vd[2k + g] V codes of key tb + 4 q4 + k, dims [64 g + 4 c16, +4)
+struct TileQ8 {
+  uint4 ka, kc;
+  uint32_t sc[4][4];
+  uint32_t vd[8];
+};
+
 // ---------------------------------------------------------------- 8-bit pass 1
-template <int SDT>
+// QUADS: the capacity is a multiple of 4, so a key quad's scales are one 128-bit load.
+template <int QDT, int SDT, bool QUADS>
 __global__ __launch_bounds__(256) void qkv_pass1_q8(DecodeParams p) {
   const int c = blockIdx.x;
   const int kvh = blockIdx.y / p.nslices, sl = blockIdx.y % p.nslices;
@@ -112,18 +151,29 @@ __global__ __launch_bounds__(256) void qkv_pass1_q8(DecodeParams p) {
   const int head0 = kvh * p.G + sl * 16;
   const int slot = p.slots ? min(max(p.slots[r], 0), p.kv_rows - 1) : r;
   const size_t tok0 = (size_t(slot) * p.KVH + kvh) * p.cap;
+  const int cap = p.cap;
+  // uniform bases of this (row, kv head)'s buffers
+  const uint32_t* __restrict__ kwr = p.kw + tok0 * 32;
+  const uint32_t* __restrict__ vwr = p.vw + tok0 * 32;
+  const uint32_t* __restrict__ ksr = static_cast<const uint32_t*>(p.ks) + tok0;
+  const uint32_t* __restrict__ kbr = static_cast<const uint32_t*>(p.kb) + tok0;
+  const uint32_t* __restrict__ vsr = static_cast<const uint32_t*>(p.vs) + tok0;
+  const uint32_t* __restrict__ vbr = static_cast<const uint32_t*>(p.vb) + tok0;
 
   // B operands of Q K^T: qb[4g + jj] = q[head c16][64g + 16q4 + 4jj + i]
   h4 qb[8];
   float qs0 = 0.0f, qs1 = 0.0f;
   {
     const bool real = c16 < Gs;
-    const size_t qrow = size_t(r) * p.H + head0 + (real ? c16 : 0);
+    const size_t qrow = (size_t(r) * p.H + head0 + (real ? c16 : 0)) * kHD;
 #pragma unroll
     for (int j = 0; j < 8; j++) {
       _Float16 t[4];
-      float& qs = j < 4 ? qs0 : qs1;
-      load_q_cols(p, qrow, real, 64 * (j >> 2) + 16 * q4 + 4 * (j & 3), t, qs);
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        t[i] = _Float16(real ? ld16<QDT>(p.q, qrow + 64 * (j >> 2) + 16 * q4 + 4 * (j & 3) + i) : 0.0f);
+        (j < 4 ? qs0 : qs1) += float(t[i]);
+      }
       qb[j] = h4{t[0], t[1], t[2], t[3]};
     }
   }
@@ -138,138 +188,137 @@ __global__ __launch_bounds__(256) void qkv_pass1_q8(DecodeParams p) {
 #pragma unroll
   for (int ii = 0; ii < 8; ii++) O[ii] = f4{0.0f, 0.0f, 0.0f, 0.0f};
 
+  // Loads are unconditional and clamped into the buffer (the keys they stand for are masked), so every path
+  // through the loop has the same loads in flight and the next tile's loads overlap this tile's arithmetic.
+  auto load = [&](int tb, TileQ8& T) {
+    const uint32_t tk = uint32_t(min(tb + c16, cap - 1));
+    T.ka = *reinterpret_cast<const uint4*>(kwr + (tk * 32u + 4u * q4));
+    T.kc = *reinterpret_cast<const uint4*>(kwr + (tk * 32u + 16u + 4u * q4));
+    if constexpr (QUADS) {
+      const uint32_t ts = uint32_t(min(tb + 4 * q4, cap - 4));
+      const uint4 a = *reinterpret_cast<const uint4*>(ksr + ts), b = *reinterpret_cast<const uint4*>(kbr + ts);
+      const uint4 x = *reinterpret_cast<const uint4*>(vsr + ts), y = *reinterpret_cast<const uint4*>(vbr + ts);
+      T.sc[0][0] = a.x; T.sc[0][1] = a.y; T.sc[0][2] = a.z; T.sc[0][3] = a.w;
+      T.sc[1][0] = b.x; T.sc[1][1] = b.y; T.sc[1][2] = b.z; T.sc[1][3] = b.w;
+      T.sc[2][0] = x.x; T.sc[2][1] = x.y; T.sc[2][2] = x.z; T.sc[2][3] = x.w;
+      T.sc[3][0] = y.x; T.sc[3][1] = y.y; T.sc[3][2] = y.z; T.sc[3][3] = y.w;
+#pragma unroll
+      for (uint32_t k = 0; k < 4; k++) {
+        T.vd[2 * k] = vwr[(ts + k) * 32u + c16];
+        T.vd[2 * k + 1] = vwr[(ts + k) * 32u + 16u + c16];
+      }
+    } else {
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        const uint32_t tt = uint32_t(min(tb + 4 * q4 + k, cap - 1));
+        T.sc[0][k] = ksr[tt];
+        T.sc[1][k] = kbr[tt];
+        T.sc[2][k] = vsr[tt];
+        T.sc[3][k] = vbr[tt];
+        T.vd[2 * k] = vwr[tt * 32u + c16];
+        T.vd[2 * k + 1] = vwr[tt * 32u + 16u + c16];
+      }
+    }
+  };
+
+  auto compute = [&](int tb, const TileQ8& T) {
+
+    // ---- S^T = K Q^T, one accumulator per 64-dim group
+    f4 a0 = f4{0.0f, 0.0f, 0.0f, 0.0f}, a1 = a0;
+    a0 = mfma16(codes4_to_h4(T.ka.x), qb[0], a0);
+    a1 = mfma16(codes4_to_h4(T.kc.x), qb[4], a1);
+    a0 = mfma16(codes4_to_h4(T.ka.y), qb[1], a0);
+    a1 = mfma16(codes4_to_h4(T.kc.y), qb[5], a1);
+    a0 = mfma16(codes4_to_h4(T.ka.z), qb[2], a0);
+    a1 = mfma16(codes4_to_h4(T.kc.z), qb[6], a1);
+    a0 = mfma16(codes4_to_h4(T.ka.w), qb[3], a0);
+    a1 = mfma16(codes4_to_h4(T.kc.w), qb[7], a1);
+
+    // ---- scores of keys tb + 4q4 + i for head c16 (base-2 logits)
+    float s[4];
+    bool valid[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int t = tb + 4 * q4 + i;
+      valid[i] = t >= tlo && t < thi;
+      const float raw = hpart<SDT>(T.sc[0][i], 0) * (a0[i] - z0) + hpart<SDT>(T.sc[0][i], 1) * (a1[i] - z1) +
+                        hpart<SDT>(T.sc[1][i], 0) * qs0 + hpart<SDT>(T.sc[1][i], 1) * qs1;
+      s[i] = valid[i] ? raw * p.scale_log2 : -INFINITY;
+    }
+    float tmax = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+    const bool need = tmax > m_run + kRescaleThr;
+    if (__any(need)) {
+      const float corr = need ? (m_run == -INFINITY ? 0.0f : fast_exp2(m_run - tmax)) : 1.0f;
+      if (need) m_run = tmax;
+      l_acc *= corr;
+      wb0 *= corr;
+      wb1 *= corr;
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const float ci = __shfl(corr, 4 * q4 + i);
+#pragma unroll
+        for (int ii = 0; ii < 8; ii++) O[ii][i] *= ci;
+      }
+    }
+    float w0[4], w1[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const float pr = valid[i] ? fast_exp2(s[i] - m_run) : 0.0f;
+      l_acc += pr;
+      w0[i] = valid[i] ? pr * hpart<SDT>(T.sc[2][i], 0) : 0.0f;
+      w1[i] = valid[i] ? pr * hpart<SDT>(T.sc[2][i], 1) : 0.0f;
+      const float pb0 = valid[i] ? pr * hpart<SDT>(T.sc[3][i], 0) : 0.0f;
+      const float pb1 = valid[i] ? pr * hpart<SDT>(T.sc[3][i], 1) : 0.0f;
+      wb0 += pb0 - 1024.0f * w0[i];
+      wb1 += pb1 - 1024.0f * w1[i];
+    }
+    uint32_t h0a, l0a, h0b, l0b, h1a, l1a, h1b, l1b;
+    split_h2(w0[0], w0[1], h0a, l0a);
+    split_h2(w0[2], w0[3], h0b, l0b);
+    split_h2(w1[0], w1[1], h1a, l1a);
+    split_h2(w1[2], w1[3], h1b, l1b);
+    const h4 A0h = pack_h4(h0a, h0b), A0l = pack_h4(l0a, l0b);
+    const h4 A1h = pack_h4(h1a, h1b), A1l = pack_h4(l1a, l1b);
+
+    // ---- O[head][64g + 4c16 + jj] += sum_k w[head][k] (1024 + V[tb + 4q4 + k][...])
+#pragma unroll
+    for (int g = 0; g < 2; g++) {
+      const uint32_t* vd = T.vd;
+      const uint32_t x01 = __builtin_amdgcn_perm(vd[2 + g], vd[g], 0x05010400u);
+      const uint32_t y01 = __builtin_amdgcn_perm(vd[2 + g], vd[g], 0x07030602u);
+      const uint32_t x23 = __builtin_amdgcn_perm(vd[6 + g], vd[4 + g], 0x05010400u);
+      const uint32_t y23 = __builtin_amdgcn_perm(vd[6 + g], vd[4 + g], 0x07030602u);
+      const h4 b0 = pack_h4(codes_to_h2(x01, 0x00050004u), codes_to_h2(x23, 0x00050004u));
+      const h4 b1 = pack_h4(codes_to_h2(x01, 0x00070006u), codes_to_h2(x23, 0x00070006u));
+      const h4 b2 = pack_h4(codes_to_h2(y01, 0x00050004u), codes_to_h2(y23, 0x00050004u));
+      const h4 b3 = pack_h4(codes_to_h2(y01, 0x00070006u), codes_to_h2(y23, 0x00070006u));
+      const h4 Ah = g ? A1h : A0h, Al = g ? A1l : A0l;
+      O[4 * g + 0] = mfma16(Ah, b0, O[4 * g + 0]);
+      O[4 * g + 1] = mfma16(Ah, b1, O[4 * g + 1]);
+      O[4 * g + 2] = mfma16(Ah, b2, O[4 * g + 2]);
+      O[4 * g + 3] = mfma16(Ah, b3, O[4 * g + 3]);
+      O[4 * g + 0] = mfma16(Al, b0, O[4 * g + 0]);
+      O[4 * g + 1] = mfma16(Al, b1, O[4 * g + 1]);
+      O[4 * g + 2] = mfma16(Al, b2, O[4 * g + 2]);
+      O[4 * g + 3] = mfma16(Al, b3, O[4 * g + 3]);
+    }
+  };
+
   if (tlo < thi) {
-    const int tb0 = tlo & ~15;
-    // tile loads: K codes of key (tb + c16), the scale/bias quads and V codes of keys tb + 4q4 + k
-    auto load_tile = [&](int tb, uint4& ka, uint4& kc, uint4& ksc, uint4& kbi, uint4& vsc, uint4& vbi,
-                         uint32_t (&vd)[8]) {
-      if (tb + 16 <= p.cap) {
-        const uint32_t* krow = p.kw + (tok0 + tb + c16) * 32;
-        ka = *reinterpret_cast<const uint4*>(krow + 4 * q4);
-        kc = *reinterpret_cast<const uint4*>(krow + 16 + 4 * q4);
-        const size_t ts = tok0 + tb + 4 * q4;
-        ksc = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(p.ks) + ts * 2);
-        kbi = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(p.kb) + ts * 2);
-        vsc = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(p.vs) + ts * 2);
-        vbi = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(p.vb) + ts * 2);
-#pragma unroll
-        for (int k = 0; k < 4; k++) {
-          vd[2 * k] = p.vw[(ts + k) * 32 + c16];
-          vd[2 * k + 1] = p.vw[(ts + k) * 32 + 16 + c16];
-        }
-      } else {  // the tile runs past the buffer's capacity: clamp each key (those keys are masked)
-        const uint32_t* krow = p.kw + (tok0 + min(tb + c16, p.cap - 1)) * 32;
-        ka = *reinterpret_cast<const uint4*>(krow + 4 * q4);
-        kc = *reinterpret_cast<const uint4*>(krow + 16 + 4 * q4);
-        uint32_t e[4][4];
-#pragma unroll
-        for (int k = 0; k < 4; k++) {
-          const size_t tt = tok0 + min(tb + 4 * q4 + k, p.cap - 1);
-          e[0][k] = static_cast<const uint32_t*>(p.ks)[tt];
-          e[1][k] = static_cast<const uint32_t*>(p.kb)[tt];
-          e[2][k] = static_cast<const uint32_t*>(p.vs)[tt];
-          e[3][k] = static_cast<const uint32_t*>(p.vb)[tt];
-          vd[2 * k] = p.vw[tt * 32 + c16];
-          vd[2 * k + 1] = p.vw[tt * 32 + 16 + c16];
-        }
-        ksc = make_uint4(e[0][0], e[0][1], e[0][2], e[0][3]);
-        kbi = make_uint4(e[1][0], e[1][1], e[1][2], e[1][3]);
-        vsc = make_uint4(e[2][0], e[2][1], e[2][2], e[2][3]);
-        vbi = make_uint4(e[3][0], e[3][1], e[3][2], e[3][3]);
-      }
-    };
-    uint4 ka, kc, ksc, kbi, vsc, vbi;
-    uint32_t vd[8];
-    load_tile(tb0, ka, kc, ksc, kbi, vsc, vbi, vd);
-    for (int tb = tb0; tb < thi; tb += 16) {
-      uint4 nka, nkc, nksc, nkbi, nvsc, nvbi;
-      uint32_t nvd[8];
-      const bool more = tb + 16 < thi;
-      if (more) load_tile(tb + 16, nka, nkc, nksc, nkbi, nvsc, nvbi, nvd);
-
-      // ---- S^T = K Q^T, one accumulator per 64-dim group
-      f4 a0 = f4{0.0f, 0.0f, 0.0f, 0.0f}, a1 = a0;
-      a0 = mfma16(codes4_to_h4(ka.x), qb[0], a0);
-      a0 = mfma16(codes4_to_h4(ka.y), qb[1], a0);
-      a0 = mfma16(codes4_to_h4(ka.z), qb[2], a0);
-      a0 = mfma16(codes4_to_h4(ka.w), qb[3], a0);
-      a1 = mfma16(codes4_to_h4(kc.x), qb[4], a1);
-      a1 = mfma16(codes4_to_h4(kc.y), qb[5], a1);
-      a1 = mfma16(codes4_to_h4(kc.z), qb[6], a1);
-      a1 = mfma16(codes4_to_h4(kc.w), qb[7], a1);
-
-      // ---- scores of keys tb + 4q4 + i for head c16 (base-2 logits)
-      const uint32_t kscw[4] = {ksc.x, ksc.y, ksc.z, ksc.w}, kbiw[4] = {kbi.x, kbi.y, kbi.z, kbi.w};
-      const uint32_t vscw[4] = {vsc.x, vsc.y, vsc.z, vsc.w}, vbiw[4] = {vbi.x, vbi.y, vbi.z, vbi.w};
-      float s[4];
-      bool valid[4];
-#pragma unroll
-      for (int i = 0; i < 4; i++) {
-        const int t = tb + 4 * q4 + i;
-        valid[i] = t >= tlo && t < thi;
-        const float raw = half_of(kscw[i], 0, SDT) * (a0[i] - z0) + half_of(kscw[i], 1, SDT) * (a1[i] - z1) +
-                          half_of(kbiw[i], 0, SDT) * qs0 + half_of(kbiw[i], 1, SDT) * qs1;
-        s[i] = valid[i] ? raw * p.scale_log2 : -INFINITY;
-      }
-      float tmax = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
-      tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
-      tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
-      const bool need = tmax > m_run + kRescaleThr;
-      if (__any(need)) {
-        const float corr = need ? (m_run == -INFINITY ? 0.0f : fast_exp2(m_run - tmax)) : 1.0f;
-        if (need) m_run = tmax;
-        l_acc *= corr;
-        wb0 *= corr;
-        wb1 *= corr;
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-          const float ci = __shfl(corr, 4 * q4 + i);
-#pragma unroll
-          for (int ii = 0; ii < 8; ii++) O[ii][i] *= ci;
-        }
-      }
-      float w0[4], w1[4];
-#pragma unroll
-      for (int i = 0; i < 4; i++) {
-        const float pr = valid[i] ? fast_exp2(s[i] - m_run) : 0.0f;
-        l_acc += pr;
-        w0[i] = valid[i] ? pr * half_of(vscw[i], 0, SDT) : 0.0f;
-        w1[i] = valid[i] ? pr * half_of(vscw[i], 1, SDT) : 0.0f;
-        const float pb0 = valid[i] ? pr * half_of(vbiw[i], 0, SDT) : 0.0f;
-        const float pb1 = valid[i] ? pr * half_of(vbiw[i], 1, SDT) : 0.0f;
-        wb0 += pb0 - 1024.0f * w0[i];
-        wb1 += pb1 - 1024.0f * w1[i];
-      }
-      uint32_t h0a, l0a, h0b, l0b, h1a, l1a, h1b, l1b;
-      split_h2(w0[0], w0[1], h0a, l0a);
-      split_h2(w0[2], w0[3], h0b, l0b);
-      split_h2(w1[0], w1[1], h1a, l1a);
-      split_h2(w1[2], w1[3], h1b, l1b);
-      const h4 A0h = pack_h4(h0a, h0b), A0l = pack_h4(l0a, l0b);
-      const h4 A1h = pack_h4(h1a, h1b), A1l = pack_h4(l1a, l1b);
-
-      // ---- O[head][64g + 4c16 + jj] += sum_k w[head][k] (1024 + V[tb + 4q4 + k][...])
-#pragma unroll
-      for (int g = 0; g < 2; g++) {
-        const uint32_t x01 = __builtin_amdgcn_perm(vd[2 + g], vd[g], 0x05010400u);
-        const uint32_t y01 = __builtin_amdgcn_perm(vd[2 + g], vd[g], 0x07030602u);
-        const uint32_t x23 = __builtin_amdgcn_perm(vd[6 + g], vd[4 + g], 0x05010400u);
-        const uint32_t y23 = __builtin_amdgcn_perm(vd[6 + g], vd[4 + g], 0x07030602u);
-        const h4 b0 = pack_h4(codes_to_h2(x01, 0x00050004u), codes_to_h2(x23, 0x00050004u));
-        const h4 b1 = pack_h4(codes_to_h2(x01, 0x00070006u), codes_to_h2(x23, 0x00070006u));
-        const h4 b2 = pack_h4(codes_to_h2(y01, 0x00050004u), codes_to_h2(y23, 0x00050004u));
-        const h4 b3 = pack_h4(codes_to_h2(y01, 0x00070006u), codes_to_h2(y23, 0x00070006u));
-        const h4 Ah = g ? A1h : A0h, Al = g ? A1l : A0l;
-        O[4 * g + 0] = mfma16(Al, b0, mfma16(Ah, b0, O[4 * g + 0]));
-        O[4 * g + 1] = mfma16(Al, b1, mfma16(Ah, b1, O[4 * g + 1]));
-        O[4 * g + 2] = mfma16(Al, b2, mfma16(Ah, b2, O[4 * g + 2]));
-        O[4 * g + 3] = mfma16(Al, b3, mfma16(Ah, b3, O[4 * g + 3]));
-      }
-      if (more) {
-        ka = nka; kc = nkc; ksc = nksc; kbi = nkbi; vsc = nvsc; vbi = nvbi;
-#pragma unroll
-        for (int k = 0; k < 8; k++) vd[k] = nvd[k];
-      }
+    const int tb0 = tlo & ~15, tbl = (thi - 1) & ~15;
+    TileQ8 A, B;  // ping-pong: the tile in flight is never copied, so no wait is forced on it
+    load(tb0, A);
+    for (int tb = tb0;;) {
+      load(min(tb + 16, tbl), B);
+      compute(tb, A);
+      tb += 16;
+      if (tb > tbl) break;
+      load(min(tb + 16, tbl), A);
+      compute(tb, B);
+      tb += 16;
+      if (tb > tbl) break;
     }
   }
 
@@ -293,32 +342,14 @@ __global__ __launch_bounds__(256) void qkv_pass1_q8(DecodeParams p) {
     for (int ii = 0; ii < 8; ii++) s_o[wave][4 * q4 + i][64 * (ii >> 2) + 4 * c16 + (ii & 3)] = O[ii][i] + (ii < 4 ? b0 : b1);
   }
   __syncthreads();
-  for (int e = threadIdx.x; e < Gs * kHD; e += 256) {
-    const int h = e >> 7, d = e & (kHD - 1);
-    float M = -INFINITY;
-#pragma unroll
-    for (int w = 0; w < kWaves; w++) M = fmaxf(M, s_m[w][h]);
-    float L = 0.0f, o = 0.0f;
-#pragma unroll
-    for (int w = 0; w < kWaves; w++) {
-      const float f = s_m[w][h] == -INFINITY ? 0.0f : fast_exp2(s_m[w][h] - M);
-      L += f * s_l[w][h];
-      o += f * s_o[w][h][d];
-    }
-    const size_t part = (size_t(r) * p.H + head0 + h) * p.nchunks + c;
-    p.po[part * kHD + d] = o;
-    if (d == 0) {
-      p.pm[part] = M;
-      p.pl[part] = L;
-    }
-  }
+  join_waves(p, s_m, s_l, s_o, Gs, r, head0, c);
 }
 
 // ------------------------------------------------------------ 16-bit pass 1
 // K/V of dtype KDT (fp16 or bf16) in (rows, KVH, cap, 128).  Q K^T: lane (key
 // c16, quad q4) supplies dims 32q4 + 4j + i of its key for MFMA j; P V: N-tile ii
 // column n is dim 8n + ii, so a lane reads 16 contiguous bytes of each of its 4 keys.
-template <int KDT>
+template <int QDT, int KDT>
 __global__ __launch_bounds__(256) void ragged_pass1_16(DecodeParams p) {
   const int c = blockIdx.x;
   const int kvh = blockIdx.y / p.nslices, sl = blockIdx.y % p.nslices;
@@ -336,20 +367,21 @@ __global__ __launch_bounds__(256) void ragged_pass1_16(DecodeParams p) {
   const int head0 = kvh * p.G + sl * 16;
   const int slot = p.slots ? min(max(p.slots[r], 0), p.kv_rows - 1) : r;
   const size_t tok0 = (size_t(slot) * p.KVH + kvh) * p.cap;
-  const uint16_t* K = static_cast<const uint16_t*>(p.kf);
-  const uint16_t* V = static_cast<const uint16_t*>(p.vf);
+  const int cap = p.cap;
+  const uint16_t* __restrict__ K = static_cast<const uint16_t*>(p.kf) + tok0 * kHD;
+  const uint16_t* __restrict__ V = static_cast<const uint16_t*>(p.vf) + tok0 * kHD;
   const float scale_log2 = p.scale_dev ? p.scale_dev[0] * kLog2e : p.scale_log2;
 
   uint32_t qb[8][2];
   {
     const bool real = c16 < Gs;
-    const size_t qrow = size_t(r) * p.H + head0 + (real ? c16 : 0);
+    const size_t qrow = (size_t(r) * p.H + head0 + (real ? c16 : 0)) * kHD;
 #pragma unroll
     for (int j = 0; j < 8; j++) {
       uint32_t bits[4];
 #pragma unroll
       for (int i = 0; i < 4; i++) {
-        const float v = real ? load_as_f32(p.q, qrow * kHD + 32 * q4 + 4 * j + i, p.qdt) : 0.0f;
+        const float v = real ? ld16<QDT>(p.q, qrow + 32 * q4 + 4 * j + i) : 0.0f;
         bits[i] = KDT == DT_BF16 ? f32_to_bf16_bits(v) : __builtin_bit_cast(uint16_t, _Float16(v));
       }
       qb[j][0] = bits[0] | (bits[1] << 16);
@@ -362,92 +394,97 @@ __global__ __launch_bounds__(256) void ragged_pass1_16(DecodeParams p) {
 #pragma unroll
   for (int ii = 0; ii < 8; ii++) O[ii] = f4{0.0f, 0.0f, 0.0f, 0.0f};
 
-  if (tlo < thi) {
-    const int tb0 = tlo & ~15;
-    auto load_tile = [&](int tb, uint4 (&kd)[4], uint4 (&vd)[4]) {
-      const int last = p.cap - 1;  // keys past the capacity (only in a row's last tile) are clamped and masked
-      const uint16_t* krow = K + (tok0 + min(tb + c16, last)) * kHD + 32 * q4;
-#pragma unroll
-      for (int u = 0; u < 4; u++) kd[u] = *reinterpret_cast<const uint4*>(krow + 8 * u);
-#pragma unroll
-      for (int k = 0; k < 4; k++)
-        vd[k] = *reinterpret_cast<const uint4*>(V + (tok0 + min(tb + 4 * q4 + k, last)) * kHD + 8 * c16);
-    };
+  struct Tile16 {
     uint4 kd[4], vd[4];
-    load_tile(tb0, kd, vd);
-    for (int tb = tb0; tb < thi; tb += 16) {
-      uint4 nkd[4], nvd[4];
-      const bool more = tb + 16 < thi;
-      if (more) load_tile(tb + 16, nkd, nvd);
-      f4 a = f4{0.0f, 0.0f, 0.0f, 0.0f};
+  };
+  auto load = [&](int tb, Tile16& T) {
+    const uint32_t tk = uint32_t(min(tb + c16, cap - 1));
 #pragma unroll
-      for (int j = 0; j < 8; j++) {
-        const uint4 u = kd[j >> 1];
-        const uint32_t w0 = (j & 1) ? u.z : u.x, w1 = (j & 1) ? u.w : u.y;
-        if (KDT == DT_BF16) a = mfma16bf(pack_s4(w0, w1), pack_s4(qb[j][0], qb[j][1]), a);
-        else a = mfma16(pack_h4(w0, w1), pack_h4(qb[j][0], qb[j][1]), a);
-      }
-      float s[4];
-      bool valid[4];
+    for (uint32_t u = 0; u < 4; u++) T.kd[u] = *reinterpret_cast<const uint4*>(K + (tk * kHD + 32u * q4 + 8u * u));
 #pragma unroll
-      for (int i = 0; i < 4; i++) {
-        const int t = tb + 4 * q4 + i;
-        valid[i] = t >= tlo && t < thi;
-        s[i] = valid[i] ? a[i] * scale_log2 : -INFINITY;
-      }
-      float tmax = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
-      tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
-      tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
-      const bool need = tmax > m_run + kRescaleThr;
-      if (__any(need)) {
-        const float corr = need ? (m_run == -INFINITY ? 0.0f : fast_exp2(m_run - tmax)) : 1.0f;
-        if (need) m_run = tmax;
-        l_acc *= corr;
+    for (int k = 0; k < 4; k++)
+      T.vd[k] = *reinterpret_cast<const uint4*>(V + (uint32_t(min(tb + 4 * q4 + k, cap - 1)) * kHD + 8u * c16));
+  };
+
+  auto compute = [&](int tb, const Tile16& T) {
+    f4 a = f4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-          const float ci = __shfl(corr, 4 * q4 + i);
+    for (int j = 0; j < 8; j++) {
+      const uint4 u = T.kd[j >> 1];
+      const uint32_t w0 = (j & 1) ? u.z : u.x, w1 = (j & 1) ? u.w : u.y;
+      if constexpr (KDT == DT_BF16) a = mfma16bf(pack_s4(w0, w1), pack_s4(qb[j][0], qb[j][1]), a);
+      else a = mfma16(pack_h4(w0, w1), pack_h4(qb[j][0], qb[j][1]), a);
+    }
+    float s[4];
+    bool valid[4];
 #pragma unroll
-          for (int ii = 0; ii < 8; ii++) O[ii][i] *= ci;
-        }
-      }
-      float pr[4];
+    for (int i = 0; i < 4; i++) {
+      const int t = tb + 4 * q4 + i;
+      valid[i] = t >= tlo && t < thi;
+      s[i] = valid[i] ? a[i] * scale_log2 : -INFINITY;
+    }
+    float tmax = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+    const bool need = tmax > m_run + kRescaleThr;
+    if (__any(need)) {
+      const float corr = need ? (m_run == -INFINITY ? 0.0f : fast_exp2(m_run - tmax)) : 1.0f;
+      if (need) m_run = tmax;
+      l_acc *= corr;
 #pragma unroll
       for (int i = 0; i < 4; i++) {
-        pr[i] = valid[i] ? fast_exp2(s[i] - m_run) : 0.0f;
-        l_acc += pr[i];
+        const float ci = __shfl(corr, 4 * q4 + i);
+#pragma unroll
+        for (int ii = 0; ii < 8; ii++) O[ii][i] *= ci;
       }
-      uint32_t ha, la, hb, lb;
-      if (KDT == DT_BF16) {
-        split_bf2(pr[0], pr[1], ha, la);
-        split_bf2(pr[2], pr[3], hb, lb);
+    }
+    float pr[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      pr[i] = valid[i] ? fast_exp2(s[i] - m_run) : 0.0f;
+      l_acc += pr[i];
+    }
+    uint32_t ha, la, hb, lb;
+    if constexpr (KDT == DT_BF16) {
+      split_bf2(pr[0], pr[1], ha, la);
+      split_bf2(pr[2], pr[3], hb, lb);
+    } else {
+      split_h2(pr[0], pr[1], ha, la);
+      split_h2(pr[2], pr[3], hb, lb);
+    }
+#pragma unroll
+    for (int ii = 0; ii < 8; ii++) {
+      const uint32_t sel = (ii & 1) ? 0x07060302u : 0x05040100u;
+      const int u = ii >> 1;
+      const uint32_t w0 = u == 0 ? T.vd[0].x : u == 1 ? T.vd[0].y : u == 2 ? T.vd[0].z : T.vd[0].w;
+      const uint32_t w1 = u == 0 ? T.vd[1].x : u == 1 ? T.vd[1].y : u == 2 ? T.vd[1].z : T.vd[1].w;
+      const uint32_t w2 = u == 0 ? T.vd[2].x : u == 1 ? T.vd[2].y : u == 2 ? T.vd[2].z : T.vd[2].w;
+      const uint32_t w3 = u == 0 ? T.vd[3].x : u == 1 ? T.vd[3].y : u == 2 ? T.vd[3].z : T.vd[3].w;
+      const uint32_t b01 = __builtin_amdgcn_perm(w1, w0, sel);
+      const uint32_t b23 = __builtin_amdgcn_perm(w3, w2, sel);
+      if constexpr (KDT == DT_BF16) {
+        O[ii] = mfma16bf(pack_s4(ha, hb), pack_s4(b01, b23), O[ii]);
+        O[ii] = mfma16bf(pack_s4(la, lb), pack_s4(b01, b23), O[ii]);
       } else {
-        split_h2(pr[0], pr[1], ha, la);
-        split_h2(pr[2], pr[3], hb, lb);
+        O[ii] = mfma16(pack_h4(ha, hb), pack_h4(b01, b23), O[ii]);
+        O[ii] = mfma16(pack_h4(la, lb), pack_h4(b01, b23), O[ii]);
       }
-      const uint32_t vw[4][4] = {{vd[0].x, vd[0].y, vd[0].z, vd[0].w},
-                                 {vd[1].x, vd[1].y, vd[1].z, vd[1].w},
-                                 {vd[2].x, vd[2].y, vd[2].z, vd[2].w},
-                                 {vd[3].x, vd[3].y, vd[3].z, vd[3].w}};
-#pragma unroll
-      for (int ii = 0; ii < 8; ii++) {
-        const uint32_t sel = (ii & 1) ? 0x07060302u : 0x05040100u;
-        const uint32_t b01 = __builtin_amdgcn_perm(vw[1][ii >> 1], vw[0][ii >> 1], sel);
-        const uint32_t b23 = __builtin_amdgcn_perm(vw[3][ii >> 1], vw[2][ii >> 1], sel);
-        if (KDT == DT_BF16) {
-          O[ii] = mfma16bf(pack_s4(ha, hb), pack_s4(b01, b23), O[ii]);
-          O[ii] = mfma16bf(pack_s4(la, lb), pack_s4(b01, b23), O[ii]);
-        } else {
-          O[ii] = mfma16(pack_h4(ha, hb), pack_h4(b01, b23), O[ii]);
-          O[ii] = mfma16(pack_h4(la, lb), pack_h4(b01, b23), O[ii]);
-        }
-      }
-      if (more) {
-#pragma unroll
-        for (int u = 0; u < 4; u++) {
-          kd[u] = nkd[u];
-          vd[u] = nvd[u];
-        }
-      }
+    }
+  };
+
+  if (tlo < thi) {
+    const int tb0 = tlo & ~15, tbl = (thi - 1) & ~15;
+    Tile16 A, B;
+    load(tb0, A);
+    for (int tb = tb0;;) {
+      load(min(tb + 16, tbl), B);
+      compute(tb, A);
+      tb += 16;
+      if (tb > tbl) break;
+      load(min(tb + 16, tbl), A);
+      compute(tb, B);
+      tb += 16;
+      if (tb > tbl) break;
     }
   }
 
@@ -465,34 +502,18 @@ __global__ __launch_bounds__(256) void ragged_pass1_16(DecodeParams p) {
     for (int ii = 0; ii < 8; ii++) s_o[wave][4 * q4 + i][8 * c16 + ii] = O[ii][i];
   }
   __syncthreads();
-  for (int e = threadIdx.x; e < Gs * kHD; e += 256) {
-    const int h = e >> 7, d = e & (kHD - 1);
-    float M = -INFINITY;
-#pragma unroll
-    for (int w = 0; w < kWaves; w++) M = fmaxf(M, s_m[w][h]);
-    float L = 0.0f, o = 0.0f;
-#pragma unroll
-    for (int w = 0; w < kWaves; w++) {
-      const float f = s_m[w][h] == -INFINITY ? 0.0f : fast_exp2(s_m[w][h] - M);
-      L += f * s_l[w][h];
-      o += f * s_o[w][h][d];
-    }
-    const size_t part = (size_t(r) * p.H + head0 + h) * p.nchunks + c;
-    p.po[part * kHD + d] = o;
-    if (d == 0) {
-      p.pm[part] = M;
-      p.pl[part] = L;
-    }
-  }
+  join_waves(p, s_m, s_l, s_o, Gs, r, head0, c);
 }
 
 // ------------------------------------------------------------------- pass 2
-// One workgroup per (row, head): 4 waves each fold every 4th chunk (online, base
-// 2), joined in LDS with the sink: M = max(sink, m_v), L = 2^(sink-M) + sum l_v 2^(m_v-M),
-// out = sum o_v 2^(m_v-M) / L (locals/qkv.py:179-208).  No key and no sink: 0.
+// One workgroup per (row, head).  M = max(sink, max_c m_c) by a block reduction,
+// then 8 chunk lanes x 32 dim lanes (4 dims each) fold w_c = 2^(m_c - M) times
+// o_c and l_c with independent loads in flight, and the 8 are summed in LDS:
+// out = sum_c w_c o_c / (2^(sink - M) + sum_c w_c l_c)  (locals/qkv.py:179-208).
+// No key and no sink: 0.
 __global__ __launch_bounds__(256) void decode_combine(CombineParams p) {
   const int rh = blockIdx.x, r = rh / p.H, head = rh % p.H;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int tid = threadIdx.x;
   int lo, hi;
   row_range(p.start, p.nkeys, p.n, p.cap, r, lo, hi);
   int cl = 0, ch = 0;
@@ -500,53 +521,91 @@ __global__ __launch_bounds__(256) void decode_combine(CombineParams p) {
     cl = lo / p.chunk;
     ch = (hi + p.chunk - 1) / p.chunk;
   }
-  float M = -INFINITY, L = 0.0f, o0 = 0.0f, o1 = 0.0f;
   const size_t base = size_t(rh) * p.nchunks;
-  for (int c = cl + wave; c < ch; c += kWaves) {
-    const float mc = p.pm[base + c], lc = p.pl[base + c];
-    const float2 oc = *reinterpret_cast<const float2*>(p.po + (base + c) * kHD + 2 * lane);
-    if (mc == -INFINITY) continue;
-    const float Mn = fmaxf(M, mc);
-    const float fo = M == -INFINITY ? 0.0f : fast_exp2(M - Mn), fn = fast_exp2(mc - Mn);
-    L = L * fo + lc * fn;
-    o0 = o0 * fo + oc.x * fn;
-    o1 = o1 * fo + oc.y * fn;
-    M = Mn;
-  }
-  __shared__ float s_m[kWaves], s_l[kWaves], s_o[kWaves][kHD];
-  if (lane == 0) {
-    s_m[wave] = M;
-    s_l[wave] = L;
-  }
-  s_o[wave][2 * lane] = o0;
-  s_o[wave][2 * lane + 1] = o1;
-  __syncthreads();
-  if (wave) return;
   const float sink = p.sinks ? p.sinks[head] * kLog2e : -INFINITY;
-  float Mt = sink;
+  float m = -INFINITY;
+  for (int cc = cl + tid; cc < ch; cc += 256) m = fmaxf(m, p.pm[base + cc]);
 #pragma unroll
-  for (int w = 0; w < kWaves; w++) Mt = fmaxf(Mt, s_m[w]);
-  float r0 = 0.0f, r1 = 0.0f;
-  if (Mt != -INFINITY) {
-    float Lt = sink == -INFINITY ? 0.0f : fast_exp2(sink - Mt);
-#pragma unroll
-    for (int w = 0; w < kWaves; w++) {
-      const float f = s_m[w] == -INFINITY ? 0.0f : fast_exp2(s_m[w] - Mt);
-      Lt += s_l[w] * f;
-      r0 += s_o[w][2 * lane] * f;
-      r1 += s_o[w][2 * lane + 1] * f;
+  for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+  __shared__ float s_red[4];
+  __shared__ float4 s_o[8][32];
+  __shared__ float s_l[8][32];
+  if ((tid & 63) == 0) s_red[tid >> 6] = m;
+  __syncthreads();
+  const float M = fmaxf(fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3])), sink);
+  const int dg = tid & 31, cs = tid >> 5;
+  float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  float L = 0.0f;
+  if (M != -INFINITY) {
+    const float4* po4 = reinterpret_cast<const float4*>(p.po);
+#pragma unroll 4
+    for (int cc = cl + cs; cc < ch; cc += 8) {
+      const float mc = p.pm[base + cc];
+      const float w = mc == -INFINITY ? 0.0f : fast_exp2(mc - M);
+      const float4 o = po4[(base + cc) * (kHD / 4) + dg];
+      acc.x += w * o.x;
+      acc.y += w * o.y;
+      acc.z += w * o.z;
+      acc.w += w * o.w;
+      L += w * p.pl[base + cc];
     }
-    r0 /= Lt;
-    r1 /= Lt;
   }
-  const size_t ob = size_t(rh) * kHD + 2 * lane;
-  store_from_f32(p.out, ob, r0, p.odt);
-  store_from_f32(p.out, ob + 1, r1, p.odt);
+  s_o[cs][dg] = acc;
+  s_l[cs][dg] = L;
+  __syncthreads();
+  if (tid >= 32) return;
+  float4 t = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  float Lt = (sink == -INFINITY || M == -INFINITY) ? 0.0f : fast_exp2(sink - M);
+#pragma unroll
+  for (int k = 0; k < 8; k++) {
+    t.x += s_o[k][tid].x;
+    t.y += s_o[k][tid].y;
+    t.z += s_o[k][tid].z;
+    t.w += s_o[k][tid].w;
+    Lt += s_l[k][tid];
+  }
+  const float inv = Lt > 0.0f ? 1.0f / Lt : 0.0f;
+  const size_t ob = size_t(rh) * kHD + 4 * tid;
+  store_from_f32(p.out, ob + 0, t.x * inv, p.odt);
+  store_from_f32(p.out, ob + 1, t.y * inv, p.odt);
+  store_from_f32(p.out, ob + 2, t.z * inv, p.odt);
+  store_from_f32(p.out, ob + 3, t.w * inv, p.odt);
 }
 
 }  // namespace lcl
 
 using namespace lcl;
+
+template <int QDT, int SDT>
+static void launch_q8_t(bool quads, dim3 grid, hipStream_t stream, hipEvent_t e0, hipEvent_t e1, const DecodeParams& p) {
+  if (quads) hipExtLaunchKernelGGL(qkv_pass1_q8<QDT, SDT, true>, grid, dim3(256), 0, stream, e0, e1, 0, p);
+  else hipExtLaunchKernelGGL(qkv_pass1_q8<QDT, SDT, false>, grid, dim3(256), 0, stream, e0, e1, 0, p);
+}
+
+static void launch_q8(int qdt, int sdt, bool quads, dim3 grid, hipStream_t stream, hipEvent_t e0, hipEvent_t e1,
+                      const DecodeParams& p) {
+  if (sdt == DT_BF16) {
+    if (qdt == DT_F16) launch_q8_t<DT_F16, DT_BF16>(quads, grid, stream, e0, e1, p);
+    else if (qdt == DT_BF16) launch_q8_t<DT_BF16, DT_BF16>(quads, grid, stream, e0, e1, p);
+    else launch_q8_t<DT_F32, DT_BF16>(quads, grid, stream, e0, e1, p);
+  } else {
+    if (qdt == DT_F16) launch_q8_t<DT_F16, DT_F16>(quads, grid, stream, e0, e1, p);
+    else if (qdt == DT_BF16) launch_q8_t<DT_BF16, DT_F16>(quads, grid, stream, e0, e1, p);
+    else launch_q8_t<DT_F32, DT_F16>(quads, grid, stream, e0, e1, p);
+  }
+}
+
+static void launch_16(int qdt, int kvdt, dim3 grid, hipStream_t stream, const DecodeParams& p) {
+  if (kvdt == DT_BF16) {
+    if (qdt == DT_F16) hipLaunchKernelGGL((ragged_pass1_16<DT_F16, DT_BF16>), grid, dim3(256), 0, stream, p);
+    else if (qdt == DT_BF16) hipLaunchKernelGGL((ragged_pass1_16<DT_BF16, DT_BF16>), grid, dim3(256), 0, stream, p);
+    else hipLaunchKernelGGL((ragged_pass1_16<DT_F32, DT_BF16>), grid, dim3(256), 0, stream, p);
+  } else {
+    if (qdt == DT_F16) hipLaunchKernelGGL((ragged_pass1_16<DT_F16, DT_F16>), grid, dim3(256), 0, stream, p);
+    else if (qdt == DT_BF16) hipLaunchKernelGGL((ragged_pass1_16<DT_BF16, DT_F16>), grid, dim3(256), 0, stream, p);
+    else hipLaunchKernelGGL((ragged_pass1_16<DT_F32, DT_F16>), grid, dim3(256), 0, stream, p);
+  }
+}
 
 static int pick_chunk(int block, int extent) {
   if (block > 0) return block;
@@ -605,8 +664,7 @@ int lcl_qkv_attend_ex(const void* q, int qdt, const uint32_t* kw, const void* ks
   if (n > 0) {
     const dim3 grid(nchunks, KVH * p.nslices, B);
     hipEvent_t e0 = static_cast<hipEvent_t>(ev_start), e1 = static_cast<hipEvent_t>(ev_stop);
-    if (sdt == DT_BF16) hipExtLaunchKernelGGL(qkv_pass1_q8<DT_BF16>, grid, dim3(256), 0, stream, e0, e1, 0, p);
-    else hipExtLaunchKernelGGL(qkv_pass1_q8<DT_F16>, grid, dim3(256), 0, stream, e0, e1, 0, p);
+    launch_q8(qdt, sdt, cap % 4 == 0, grid, stream, e0, e1, p);
   }
   CombineParams c{};
   c.pm = p.pm; c.pl = p.pl; c.po = p.po; c.sinks = sinks; c.out = out;
@@ -642,8 +700,7 @@ int lcl_ragged_attention(const void* q, int qdt, const void* keys, const void* v
   p.scale_dev = scale_dev;
   p.qdt = qdt; p.sdt = kvdt;
   const dim3 grid(nchunks, Hkv * p.nslices, R);
-  if (kvdt == DT_BF16) hipLaunchKernelGGL(ragged_pass1_16<DT_BF16>, grid, dim3(256), 0, stream, p);
-  else hipLaunchKernelGGL(ragged_pass1_16<DT_F16>, grid, dim3(256), 0, stream, p);
+  launch_16(qdt, kvdt, grid, stream, p);
   CombineParams c{};
   c.pm = p.pm; c.pl = p.pl; c.po = p.po; c.sinks = nullptr; c.out = out;
   c.start = nullptr; c.nkeys = nkeys; c.n = cap; c.cap = cap; c.H = H; c.nchunks = nchunks; c.chunk = chunk;
