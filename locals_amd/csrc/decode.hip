@@ -134,7 +134,8 @@ struct TileQ8 {
 // ---------------------------------------------------------------- 8-bit pass 1
 // QUADS: the capacity is a multiple of 4, so a key quad's scales are one 128-bit load.
 template <int QDT, int SDT, bool QUADS>
-__global__ __launch_bounds__(256) void qkv_pass1_q8(DecodeParams p) {
+// 3 waves a SIMD (<= 168 VGPRs): with one tile in flight per wave that keeps ~50 KB of loads in flight per CU.
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) void qkv_pass1_q8(DecodeParams p) {
   const int c = blockIdx.x;
   const int kvh = blockIdx.y / p.nslices, sl = blockIdx.y % p.nslices;
   const int r = blockIdx.z;
@@ -350,7 +351,7 @@ __global__ __launch_bounds__(256) void qkv_pass1_q8(DecodeParams p) {
 // c16, quad q4) supplies dims 32q4 + 4j + i of its key for MFMA j; P V: N-tile ii
 // column n is dim 8n + ii, so a lane reads 16 contiguous bytes of each of its 4 keys.
 template <int QDT, int KDT>
-__global__ __launch_bounds__(256) void ragged_pass1_16(DecodeParams p) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) void ragged_pass1_16(DecodeParams p) {
   const int c = blockIdx.x;
   const int kvh = blockIdx.y / p.nslices, sl = blockIdx.y % p.nslices;
   const int r = blockIdx.z;
@@ -506,13 +507,15 @@ __global__ __launch_bounds__(256) void ragged_pass1_16(DecodeParams p) {
 }
 
 // ------------------------------------------------------------------- pass 2
-// One workgroup per (row, head).  M = max(sink, max_c m_c) by a block reduction,
-// then 8 chunk lanes x 32 dim lanes (4 dims each) fold w_c = 2^(m_c - M) times
-// o_c and l_c with independent loads in flight, and the 8 are summed in LDS:
+// Grid (row x head, 4 slices of 32 dims).  M = max(sink, max_c m_c) by a block
+// reduction; then 32 chunk lanes x 8 dim lanes (4 dims each) fold w_c = 2^(m_c - M)
+// times o_c and l_c with independent loads in flight, summed in LDS:
 // out = sum_c w_c o_c / (2^(sink - M) + sum_c w_c l_c)  (locals/qkv.py:179-208).
 // No key and no sink: 0.
+constexpr int kCombSlices = 4;
 __global__ __launch_bounds__(256) void decode_combine(CombineParams p) {
   const int rh = blockIdx.x, r = rh / p.H, head = rh % p.H;
+  const int ds = blockIdx.y;
   const int tid = threadIdx.x;
   int lo, hi;
   row_range(p.start, p.nkeys, p.n, p.cap, r, lo, hi);
@@ -528,21 +531,21 @@ __global__ __launch_bounds__(256) void decode_combine(CombineParams p) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
   __shared__ float s_red[4];
-  __shared__ float4 s_o[8][32];
-  __shared__ float s_l[8][32];
+  __shared__ float4 s_o[32][8];
+  __shared__ float s_l[32];
   if ((tid & 63) == 0) s_red[tid >> 6] = m;
   __syncthreads();
   const float M = fmaxf(fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3])), sink);
-  const int dg = tid & 31, cs = tid >> 5;
+  const int dl = tid & 7, cs = tid >> 3;
   float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
   float L = 0.0f;
   if (M != -INFINITY) {
-    const float4* po4 = reinterpret_cast<const float4*>(p.po);
+    const float4* po4 = reinterpret_cast<const float4*>(p.po) + ds * 8 + dl;
 #pragma unroll 4
-    for (int cc = cl + cs; cc < ch; cc += 8) {
+    for (int cc = cl + cs; cc < ch; cc += 32) {
       const float mc = p.pm[base + cc];
       const float w = mc == -INFINITY ? 0.0f : fast_exp2(mc - M);
-      const float4 o = po4[(base + cc) * (kHD / 4) + dg];
+      const float4 o = po4[(base + cc) * (kHD / 4)];
       acc.x += w * o.x;
       acc.y += w * o.y;
       acc.z += w * o.z;
@@ -550,22 +553,22 @@ __global__ __launch_bounds__(256) void decode_combine(CombineParams p) {
       L += w * p.pl[base + cc];
     }
   }
-  s_o[cs][dg] = acc;
-  s_l[cs][dg] = L;
+  s_o[cs][dl] = acc;
+  if (dl == 0) s_l[cs] = L;
   __syncthreads();
-  if (tid >= 32) return;
+  if (tid >= 8) return;
   float4 t = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
   float Lt = (sink == -INFINITY || M == -INFINITY) ? 0.0f : fast_exp2(sink - M);
-#pragma unroll
-  for (int k = 0; k < 8; k++) {
+#pragma unroll 8
+  for (int k = 0; k < 32; k++) {
     t.x += s_o[k][tid].x;
     t.y += s_o[k][tid].y;
     t.z += s_o[k][tid].z;
     t.w += s_o[k][tid].w;
-    Lt += s_l[k][tid];
+    Lt += s_l[k];
   }
   const float inv = Lt > 0.0f ? 1.0f / Lt : 0.0f;
-  const size_t ob = size_t(rh) * kHD + 4 * tid;
+  const size_t ob = size_t(rh) * kHD + 32 * ds + 4 * tid;
   store_from_f32(p.out, ob + 0, t.x * inv, p.odt);
   store_from_f32(p.out, ob + 1, t.y * inv, p.odt);
   store_from_f32(p.out, ob + 2, t.z * inv, p.odt);
@@ -669,7 +672,7 @@ int lcl_qkv_attend_ex(const void* q, int qdt, const uint32_t* kw, const void* ks
   CombineParams c{};
   c.pm = p.pm; c.pl = p.pl; c.po = p.po; c.sinks = sinks; c.out = out;
   c.start = start; c.nkeys = nullptr; c.n = n; c.cap = cap; c.H = H; c.nchunks = nchunks; c.chunk = chunk; c.odt = qdt;
-  hipLaunchKernelGGL(decode_combine, dim3(B * H), dim3(256), 0, stream, c);
+  hipLaunchKernelGGL(decode_combine, dim3(B * H, kCombSlices), dim3(256), 0, stream, c);
   return int(hipGetLastError());
 }
 
@@ -705,7 +708,7 @@ int lcl_ragged_attention(const void* q, int qdt, const void* keys, const void* v
   c.pm = p.pm; c.pl = p.pl; c.po = p.po; c.sinks = nullptr; c.out = out;
   c.start = nullptr; c.nkeys = nkeys; c.n = cap; c.cap = cap; c.H = H; c.nchunks = nchunks; c.chunk = chunk;
   c.odt = qdt;
-  hipLaunchKernelGGL(decode_combine, dim3(R * H), dim3(256), 0, stream, c);
+  hipLaunchKernelGGL(decode_combine, dim3(R * H, kCombSlices), dim3(256), 0, stream, c);
   return int(hipGetLastError());
 }
 
