@@ -164,8 +164,12 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--config", default="c2")
     ap.add_argument("--sets", type=int, default=2)
+    ap.add_argument("--block", type=int, default=None, help="keys a pass-1 workgroup reads (qkv.BLOCK)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
+                    help="instead of the bench: K device copies of MIB MiB (the known-size kernel that scales the "
+                         "rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (each GPU box here has one GPU); "
@@ -178,7 +182,25 @@ def main():
     from locals_amd import _lib, qkv
 
     dev = torch.device("cuda:0")
+    if args.calibrate_copy:
+        n = args.calibrate_copy << 20
+        src = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(args.steps):
+            dst.copy_(src)
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / args.steps
+        print(json.dumps({"calibrate_copy_bytes": n, "dispatches": args.steps, "ms_per_copy": round(ms, 4),
+                          "copy_GBs_read_plus_write": round(2 * n / ms / 1e6, 1)}), flush=True)
+        return
     cfg = config(args.config)
+    if args.block is not None:
+        qkv.BLOCK = args.block
     sets, start, n, cap = build_sets(cfg, args.sets, dev)
     B, H, KVH = cfg["B"], cfg["H"], cfg["KVH"]
     lib = _lib.load()

@@ -33,6 +33,8 @@
 
 #include <hip/hip_ext.h>
 
+#include <type_traits>
+
 #include "lcl_common.h"
 #include "locals_amd.h"
 
@@ -126,15 +128,19 @@ __device__ __forceinline__ float hpart(uint32_t w, int k) {
 //  sc[j][k] for keys tb + 4 q4 + k: j = 0 K scales, 1 K biases, 2 V scales, 3 V biases (a 16-bit pair a key)
 //  vd[2k + g] V codes of key tb + 4 q4 + k, dims [64 g + 4 c16, +4)
 struct TileQ8 {
-  uint4 ka, kc;
-  uint32_t sc[4][4];
+  u4 ka, kc;
+  u4 sc[4];
   uint32_t vd[8];
 };
 
 // ---------------------------------------------------------------- 8-bit pass 1
-// QUADS: the capacity is a multiple of 4, so a key quad's scales are one 128-bit load.
-template <int QDT, int SDT, bool QUADS>
-// 3 waves a SIMD (<= 168 VGPRs): with one tile in flight per wave that keeps ~50 KB of loads in flight per CU.
+// Loads are raw buffer loads: one descriptor per array of this (row, kv head), a per-lane
+// offset fixed for the whole loop plus the tile's, so a tile's addressing is 3 VALU adds,
+// and keys past the capacity read 0 (they are masked).  Tiles wholly inside the wave's
+// key range take a path without masking.
+// 3 waves a SIMD (<= 168 VGPRs): with one tile in flight per wave that keeps ~50 KB of
+// loads in flight per CU.
+template <int QDT, int SDT>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) void qkv_pass1_q8(DecodeParams p) {
   const int c = blockIdx.x;
   const int kvh = blockIdx.y / p.nslices, sl = blockIdx.y % p.nslices;
@@ -147,19 +153,46 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int c16 = lane & 15, q4 = lane >> 4;
   const int sub = p.chunk / kWaves;
-  const int tlo = max(lo, c0 + wave * sub), thi = min(hi, c0 + (wave + 1) * sub);
+  const int wlo = c0 + wave * sub, whi = c0 + (wave + 1) * sub;
+  const int tlo = max(lo, wlo), thi = min(hi, whi);
   const int Gs = min(16, p.G - sl * 16);
   const int head0 = kvh * p.G + sl * 16;
   const int slot = p.slots ? min(max(p.slots[r], 0), p.kv_rows - 1) : r;
   const size_t tok0 = (size_t(slot) * p.KVH + kvh) * p.cap;
   const int cap = p.cap;
-  // uniform bases of this (row, kv head)'s buffers
-  const uint32_t* __restrict__ kwr = p.kw + tok0 * 32;
-  const uint32_t* __restrict__ vwr = p.vw + tok0 * 32;
-  const uint32_t* __restrict__ ksr = static_cast<const uint32_t*>(p.ks) + tok0;
-  const uint32_t* __restrict__ kbr = static_cast<const uint32_t*>(p.kb) + tok0;
-  const uint32_t* __restrict__ vsr = static_cast<const uint32_t*>(p.vs) + tok0;
-  const uint32_t* __restrict__ vbr = static_cast<const uint32_t*>(p.vb) + tok0;
+  const BufRsrc rk = make_rsrc(p.kw + tok0 * 32, uint32_t(cap) * 128u);
+  const BufRsrc rv = make_rsrc(p.vw + tok0 * 32, uint32_t(cap) * 128u);
+  const BufRsrc rks = make_rsrc(static_cast<const uint32_t*>(p.ks) + tok0, uint32_t(cap) * 4u);
+  const BufRsrc rkb = make_rsrc(static_cast<const uint32_t*>(p.kb) + tok0, uint32_t(cap) * 4u);
+  const BufRsrc rvs = make_rsrc(static_cast<const uint32_t*>(p.vs) + tok0, uint32_t(cap) * 4u);
+  const BufRsrc rvb = make_rsrc(static_cast<const uint32_t*>(p.vb) + tok0, uint32_t(cap) * 4u);
+  const uint32_t offK = uint32_t(c16) * 128u + 16u * q4;  // + tb * 128
+  const uint32_t offS = 16u * q4;                          // + tb * 4
+  const uint32_t offV = uint32_t(q4) * 512u + 4u * c16;    // + tb * 128
+
+  auto load = [&](int tb, TileQ8& T) {
+    const uint32_t k = uint32_t(tb) * 128u, s4 = uint32_t(tb) * 4u;
+    T.ka = buf_load_b128(rk, offK + k, 0);
+    T.kc = buf_load_b128(rk, offK + k, 64);
+    T.sc[0] = buf_load_b128(rks, offS + s4, 0);
+    T.sc[1] = buf_load_b128(rkb, offS + s4, 0);
+    T.sc[2] = buf_load_b128(rvs, offS + s4, 0);
+    T.sc[3] = buf_load_b128(rvb, offS + s4, 0);
+    const uint32_t v = offV + k;
+    T.vd[0] = buf_load_b32(rv, v, 0);
+    T.vd[1] = buf_load_b32(rv, v, 64);
+    T.vd[2] = buf_load_b32(rv, v, 128);
+    T.vd[3] = buf_load_b32(rv, v, 192);
+    T.vd[4] = buf_load_b32(rv, v, 256);
+    T.vd[5] = buf_load_b32(rv, v, 320);
+    T.vd[6] = buf_load_b32(rv, v, 384);
+    T.vd[7] = buf_load_b32(rv, v, 448);
+  };
+
+  // the first tile's loads go out before the query is read, so their latency overlaps the prologue
+  TileQ8 A, B;  // ping-pong: the tile in flight is never copied, so no wait is forced on it
+  const int tb0 = tlo & ~15, tbl = (thi - 1) & ~15;
+  if (tlo < thi) load(tb0, A);
 
   // B operands of Q K^T: qb[4g + jj] = q[head c16][64g + 16q4 + 4jj + i]
   h4 qb[8];
@@ -182,48 +215,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
   qs0 += __shfl_xor(qs0, 32);
   qs1 += __shfl_xor(qs1, 16);
   qs1 += __shfl_xor(qs1, 32);
-  const float z0 = 1024.0f * qs0, z1 = 1024.0f * qs1;
+  // base-2 logits: s = C (sc0 (a0 - 1024 Qs0) + sc1 (a1 - 1024 Qs1) + b0 Qs0 + b1 Qs1), C = scale log2 e
+  const float C = p.scale_log2;
+  const float zc0 = 1024.0f * qs0 * C, zc1 = 1024.0f * qs1 * C, qc0 = qs0 * C, qc1 = qs1 * C;
 
   float m_run = -INFINITY, l_acc = 0.0f, wb0 = 0.0f, wb1 = 0.0f;
   f4 O[8];
 #pragma unroll
   for (int ii = 0; ii < 8; ii++) O[ii] = f4{0.0f, 0.0f, 0.0f, 0.0f};
 
-  // Loads are unconditional and clamped into the buffer (the keys they stand for are masked), so every path
-  // through the loop has the same loads in flight and the next tile's loads overlap this tile's arithmetic.
-  auto load = [&](int tb, TileQ8& T) {
-    const uint32_t tk = uint32_t(min(tb + c16, cap - 1));
-    T.ka = *reinterpret_cast<const uint4*>(kwr + (tk * 32u + 4u * q4));
-    T.kc = *reinterpret_cast<const uint4*>(kwr + (tk * 32u + 16u + 4u * q4));
-    if constexpr (QUADS) {
-      const uint32_t ts = uint32_t(min(tb + 4 * q4, cap - 4));
-      const uint4 a = *reinterpret_cast<const uint4*>(ksr + ts), b = *reinterpret_cast<const uint4*>(kbr + ts);
-      const uint4 x = *reinterpret_cast<const uint4*>(vsr + ts), y = *reinterpret_cast<const uint4*>(vbr + ts);
-      T.sc[0][0] = a.x; T.sc[0][1] = a.y; T.sc[0][2] = a.z; T.sc[0][3] = a.w;
-      T.sc[1][0] = b.x; T.sc[1][1] = b.y; T.sc[1][2] = b.z; T.sc[1][3] = b.w;
-      T.sc[2][0] = x.x; T.sc[2][1] = x.y; T.sc[2][2] = x.z; T.sc[2][3] = x.w;
-      T.sc[3][0] = y.x; T.sc[3][1] = y.y; T.sc[3][2] = y.z; T.sc[3][3] = y.w;
-#pragma unroll
-      for (uint32_t k = 0; k < 4; k++) {
-        T.vd[2 * k] = vwr[(ts + k) * 32u + c16];
-        T.vd[2 * k + 1] = vwr[(ts + k) * 32u + 16u + c16];
-      }
-    } else {
-#pragma unroll
-      for (int k = 0; k < 4; k++) {
-        const uint32_t tt = uint32_t(min(tb + 4 * q4 + k, cap - 1));
-        T.sc[0][k] = ksr[tt];
-        T.sc[1][k] = kbr[tt];
-        T.sc[2][k] = vsr[tt];
-        T.sc[3][k] = vbr[tt];
-        T.vd[2 * k] = vwr[tt * 32u + c16];
-        T.vd[2 * k + 1] = vwr[tt * 32u + 16u + c16];
-      }
-    }
-  };
-
-  auto compute = [&](int tb, const TileQ8& T) {
-
+  auto compute = [&](int tb, const TileQ8& T, auto masked) {
+    constexpr bool MASKED = decltype(masked)::value;
     // ---- S^T = K Q^T, one accumulator per 64-dim group
     f4 a0 = f4{0.0f, 0.0f, 0.0f, 0.0f}, a1 = a0;
     a0 = mfma16(codes4_to_h4(T.ka.x), qb[0], a0);
@@ -235,16 +237,42 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
     a0 = mfma16(codes4_to_h4(T.ka.w), qb[3], a0);
     a1 = mfma16(codes4_to_h4(T.kc.w), qb[7], a1);
 
+    // ---- V codes as the B operands of P V (keys tb + 4q4 + k, dims 64g + 4c16 + jj)
+    h4 bv[8];
+#pragma unroll
+    for (int g = 0; g < 2; g++) {
+      const uint32_t x01 = __builtin_amdgcn_perm(T.vd[2 + g], T.vd[g], 0x05010400u);
+      const uint32_t y01 = __builtin_amdgcn_perm(T.vd[2 + g], T.vd[g], 0x07030602u);
+      const uint32_t x23 = __builtin_amdgcn_perm(T.vd[6 + g], T.vd[4 + g], 0x05010400u);
+      const uint32_t y23 = __builtin_amdgcn_perm(T.vd[6 + g], T.vd[4 + g], 0x07030602u);
+      bv[4 * g + 0] = pack_h4(codes_to_h2(x01, 0x00050004u), codes_to_h2(x23, 0x00050004u));
+      bv[4 * g + 1] = pack_h4(codes_to_h2(x01, 0x00070006u), codes_to_h2(x23, 0x00070006u));
+      bv[4 * g + 2] = pack_h4(codes_to_h2(y01, 0x00050004u), codes_to_h2(y23, 0x00050004u));
+      bv[4 * g + 3] = pack_h4(codes_to_h2(y01, 0x00070006u), codes_to_h2(y23, 0x00070006u));
+    }
+
     // ---- scores of keys tb + 4q4 + i for head c16 (base-2 logits)
+    const uint32_t ksc[4] = {T.sc[0].x, T.sc[0].y, T.sc[0].z, T.sc[0].w};
+    const uint32_t kbi[4] = {T.sc[1].x, T.sc[1].y, T.sc[1].z, T.sc[1].w};
+    const uint32_t vsc[4] = {T.sc[2].x, T.sc[2].y, T.sc[2].z, T.sc[2].w};
+    const uint32_t vbi[4] = {T.sc[3].x, T.sc[3].y, T.sc[3].z, T.sc[3].w};
     float s[4];
     bool valid[4];
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-      const int t = tb + 4 * q4 + i;
-      valid[i] = t >= tlo && t < thi;
-      const float raw = hpart<SDT>(T.sc[0][i], 0) * (a0[i] - z0) + hpart<SDT>(T.sc[0][i], 1) * (a1[i] - z1) +
-                        hpart<SDT>(T.sc[1][i], 0) * qs0 + hpart<SDT>(T.sc[1][i], 1) * qs1;
-      s[i] = valid[i] ? raw * p.scale_log2 : -INFINITY;
+      const float u0 = __builtin_fmaf(a0[i], C, -zc0), u1 = __builtin_fmaf(a1[i], C, -zc1);
+      float v = hpart<SDT>(ksc[i], 0) * u0;
+      v = __builtin_fmaf(hpart<SDT>(ksc[i], 1), u1, v);
+      v = __builtin_fmaf(hpart<SDT>(kbi[i], 0), qc0, v);
+      v = __builtin_fmaf(hpart<SDT>(kbi[i], 1), qc1, v);
+      if constexpr (MASKED) {
+        const int t = tb + 4 * q4 + i;
+        valid[i] = t >= tlo && t < thi;
+        s[i] = valid[i] ? v : -INFINITY;
+      } else {
+        valid[i] = true;
+        s[i] = v;
+      }
     }
     float tmax = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
     tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
@@ -266,14 +294,21 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
     float w0[4], w1[4];
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-      const float pr = valid[i] ? fast_exp2(s[i] - m_run) : 0.0f;
+      float pr = fast_exp2(s[i] - m_run);
+      float x0 = pr * hpart<SDT>(vsc[i], 0), x1 = pr * hpart<SDT>(vsc[i], 1);
+      float y0 = pr * hpart<SDT>(vbi[i], 0), y1 = pr * hpart<SDT>(vbi[i], 1);
+      if constexpr (MASKED) {  // garbage scales of masked keys must not reach the sums (0 * inf)
+        pr = valid[i] ? pr : 0.0f;
+        x0 = valid[i] ? x0 : 0.0f;
+        x1 = valid[i] ? x1 : 0.0f;
+        y0 = valid[i] ? y0 : 0.0f;
+        y1 = valid[i] ? y1 : 0.0f;
+      }
       l_acc += pr;
-      w0[i] = valid[i] ? pr * hpart<SDT>(T.sc[2][i], 0) : 0.0f;
-      w1[i] = valid[i] ? pr * hpart<SDT>(T.sc[2][i], 1) : 0.0f;
-      const float pb0 = valid[i] ? pr * hpart<SDT>(T.sc[3][i], 0) : 0.0f;
-      const float pb1 = valid[i] ? pr * hpart<SDT>(T.sc[3][i], 1) : 0.0f;
-      wb0 += pb0 - 1024.0f * w0[i];
-      wb1 += pb1 - 1024.0f * w1[i];
+      w0[i] = x0;
+      w1[i] = x1;
+      wb0 += __builtin_fmaf(-1024.0f, x0, y0);
+      wb1 += __builtin_fmaf(-1024.0f, x1, y1);
     }
     uint32_t h0a, l0a, h0b, l0b, h1a, l1a, h1b, l1b;
     split_h2(w0[0], w0[1], h0a, l0a);
@@ -285,39 +320,27 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
 
     // ---- O[head][64g + 4c16 + jj] += sum_k w[head][k] (1024 + V[tb + 4q4 + k][...])
 #pragma unroll
-    for (int g = 0; g < 2; g++) {
-      const uint32_t* vd = T.vd;
-      const uint32_t x01 = __builtin_amdgcn_perm(vd[2 + g], vd[g], 0x05010400u);
-      const uint32_t y01 = __builtin_amdgcn_perm(vd[2 + g], vd[g], 0x07030602u);
-      const uint32_t x23 = __builtin_amdgcn_perm(vd[6 + g], vd[4 + g], 0x05010400u);
-      const uint32_t y23 = __builtin_amdgcn_perm(vd[6 + g], vd[4 + g], 0x07030602u);
-      const h4 b0 = pack_h4(codes_to_h2(x01, 0x00050004u), codes_to_h2(x23, 0x00050004u));
-      const h4 b1 = pack_h4(codes_to_h2(x01, 0x00070006u), codes_to_h2(x23, 0x00070006u));
-      const h4 b2 = pack_h4(codes_to_h2(y01, 0x00050004u), codes_to_h2(y23, 0x00050004u));
-      const h4 b3 = pack_h4(codes_to_h2(y01, 0x00070006u), codes_to_h2(y23, 0x00070006u));
-      const h4 Ah = g ? A1h : A0h, Al = g ? A1l : A0l;
-      O[4 * g + 0] = mfma16(Ah, b0, O[4 * g + 0]);
-      O[4 * g + 1] = mfma16(Ah, b1, O[4 * g + 1]);
-      O[4 * g + 2] = mfma16(Ah, b2, O[4 * g + 2]);
-      O[4 * g + 3] = mfma16(Ah, b3, O[4 * g + 3]);
-      O[4 * g + 0] = mfma16(Al, b0, O[4 * g + 0]);
-      O[4 * g + 1] = mfma16(Al, b1, O[4 * g + 1]);
-      O[4 * g + 2] = mfma16(Al, b2, O[4 * g + 2]);
-      O[4 * g + 3] = mfma16(Al, b3, O[4 * g + 3]);
+    for (int jj = 0; jj < 4; jj++) {
+      O[jj] = mfma16(A0h, bv[jj], O[jj]);
+      O[4 + jj] = mfma16(A1h, bv[4 + jj], O[4 + jj]);
+    }
+#pragma unroll
+    for (int jj = 0; jj < 4; jj++) {
+      O[jj] = mfma16(A0l, bv[jj], O[jj]);
+      O[4 + jj] = mfma16(A1l, bv[4 + jj], O[4 + jj]);
     }
   };
 
   if (tlo < thi) {
-    const int tb0 = tlo & ~15, tbl = (thi - 1) & ~15;
-    TileQ8 A, B;  // ping-pong: the tile in flight is never copied, so no wait is forced on it
-    load(tb0, A);
     for (int tb = tb0;;) {
       load(min(tb + 16, tbl), B);
-      compute(tb, A);
+      if (tb >= tlo && tb + 16 <= thi) compute(tb, A, std::false_type{});
+      else compute(tb, A, std::true_type{});
       tb += 16;
       if (tb > tbl) break;
       load(min(tb + 16, tbl), A);
-      compute(tb, B);
+      if (tb >= tlo && tb + 16 <= thi) compute(tb, B, std::false_type{});
+      else compute(tb, B, std::true_type{});
       tb += 16;
       if (tb > tbl) break;
     }
@@ -580,21 +603,20 @@ __global__ __launch_bounds__(256) void decode_combine(CombineParams p) {
 using namespace lcl;
 
 template <int QDT, int SDT>
-static void launch_q8_t(bool quads, dim3 grid, hipStream_t stream, hipEvent_t e0, hipEvent_t e1, const DecodeParams& p) {
-  if (quads) hipExtLaunchKernelGGL(qkv_pass1_q8<QDT, SDT, true>, grid, dim3(256), 0, stream, e0, e1, 0, p);
-  else hipExtLaunchKernelGGL(qkv_pass1_q8<QDT, SDT, false>, grid, dim3(256), 0, stream, e0, e1, 0, p);
+static void launch_q8_t(dim3 grid, hipStream_t stream, hipEvent_t e0, hipEvent_t e1, const DecodeParams& p) {
+  hipExtLaunchKernelGGL((qkv_pass1_q8<QDT, SDT>), grid, dim3(256), 0, stream, e0, e1, 0, p);
 }
 
-static void launch_q8(int qdt, int sdt, bool quads, dim3 grid, hipStream_t stream, hipEvent_t e0, hipEvent_t e1,
+static void launch_q8(int qdt, int sdt, dim3 grid, hipStream_t stream, hipEvent_t e0, hipEvent_t e1,
                       const DecodeParams& p) {
   if (sdt == DT_BF16) {
-    if (qdt == DT_F16) launch_q8_t<DT_F16, DT_BF16>(quads, grid, stream, e0, e1, p);
-    else if (qdt == DT_BF16) launch_q8_t<DT_BF16, DT_BF16>(quads, grid, stream, e0, e1, p);
-    else launch_q8_t<DT_F32, DT_BF16>(quads, grid, stream, e0, e1, p);
+    if (qdt == DT_F16) launch_q8_t<DT_F16, DT_BF16>(grid, stream, e0, e1, p);
+    else if (qdt == DT_BF16) launch_q8_t<DT_BF16, DT_BF16>(grid, stream, e0, e1, p);
+    else launch_q8_t<DT_F32, DT_BF16>(grid, stream, e0, e1, p);
   } else {
-    if (qdt == DT_F16) launch_q8_t<DT_F16, DT_F16>(quads, grid, stream, e0, e1, p);
-    else if (qdt == DT_BF16) launch_q8_t<DT_BF16, DT_F16>(quads, grid, stream, e0, e1, p);
-    else launch_q8_t<DT_F32, DT_F16>(quads, grid, stream, e0, e1, p);
+    if (qdt == DT_F16) launch_q8_t<DT_F16, DT_F16>(grid, stream, e0, e1, p);
+    else if (qdt == DT_BF16) launch_q8_t<DT_BF16, DT_F16>(grid, stream, e0, e1, p);
+    else launch_q8_t<DT_F32, DT_F16>(grid, stream, e0, e1, p);
   }
 }
 
@@ -667,7 +689,7 @@ int lcl_qkv_attend_ex(const void* q, int qdt, const uint32_t* kw, const void* ks
   if (n > 0) {
     const dim3 grid(nchunks, KVH * p.nslices, B);
     hipEvent_t e0 = static_cast<hipEvent_t>(ev_start), e1 = static_cast<hipEvent_t>(ev_stop);
-    launch_q8(qdt, sdt, cap % 4 == 0, grid, stream, e0, e1, p);
+    launch_q8(qdt, sdt, grid, stream, e0, e1, p);
   }
   CombineParams c{};
   c.pm = p.pm; c.pl = p.pl; c.po = p.po; c.sinks = sinks; c.out = out;

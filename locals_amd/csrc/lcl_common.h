@@ -91,7 +91,7 @@ __device__ __forceinline__ uint32_t pkrtz(float a, float b) {
 __device__ __forceinline__ void split_h2(float a, float b, uint32_t& hi, uint32_t& lo) {
   hi = pkrtz(a, b);
   const h2 h = __builtin_bit_cast(h2, hi);
-  lo = pkrtz(a - float(h.x), b - float(h.y));
+  lo = pkrtz(__builtin_fmaf(float(h.x), -1.0f, a), __builtin_fmaf(float(h.y), -1.0f, b));
 }
 
 // bf16 pair by truncation: hi = top 16 bits, lo = top 16 bits of the remainder
@@ -103,5 +103,29 @@ __device__ __forceinline__ void split_bf2(float a, float b, uint32_t& hi, uint32
 }
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+typedef __amdgpu_buffer_rsrc_t BufRsrc;
+
+// Raw buffer descriptor over `bytes` bytes at p (gfx9 word 3: 32-bit data format, as CK uses
+// for gfx90a/gfx94x/gfx950).  Loads at offsets >= bytes return 0; the range check covers the
+// VGPR offset and the instruction offset, so callers keep every variable part there.
+__device__ __forceinline__ BufRsrc make_rsrc(const void* p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, int(bytes), 0x00020000);
+}
+
+// Cache policy of a load (gfx950): 0 = default, kNT = non-temporal (aux bit 1, `nt`).  Measured
+// on an MI355X, a stream of whole 128-byte lines per instruction reaches ~7.0 TB/s with `nt`
+// against ~6.0 TB/s without; but where two instructions each take half of the same lines (the
+// register-fed decode tiles) `nt` costs ~12%, so those loads keep the default policy.
+constexpr int kNT = 2;
+
+__device__ __forceinline__ u4 buf_load_b128(BufRsrc r, uint32_t voff, const int imm) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, int(voff + uint32_t(imm)), 0, 0);
+}
+
+__device__ __forceinline__ uint32_t buf_load_b32(BufRsrc r, uint32_t voff, const int imm) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, int(voff + uint32_t(imm)), 0, 0);
+}
 
 }  // namespace lcl
