@@ -1,0 +1,127 @@
+"""CPU checks of the boundary: the C-ABI library loads and exports every entry point include/*.h declares, the
+Python signature table matches the header, entry points reject bad arguments before touching the GPU, and the
+host-side cache bookkeeping (mlx-lm BatchKVCache semantics, locals/qkv.py:295-452) is right on CPU tensors."""
+
+import ctypes
+import glob
+import os
+import re
+
+import numpy as np
+import pytest
+import torch
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _declared():
+    names = set()
+    for h in glob.glob(os.path.join(ROOT, "include", "*.h")):
+        src = open(h).read()
+        names |= set(re.findall(r"^\s*(?:int|size_t|void)\s+(lcl_\w+)\s*\(", src, re.M))
+    return names
+
+
+def test_library_exports_every_declared_symbol():
+    from locals_amd import _lib
+
+    lib = _lib.load()
+    declared = _declared()
+    assert declared, "no declarations found"
+    for name in declared:
+        assert hasattr(lib, name), name
+    assert declared == set(_lib.SIGNATURES), declared ^ set(_lib.SIGNATURES)
+
+
+def test_signature_arity_matches_header():
+    from locals_amd import _lib
+
+    src = "".join(open(h).read() for h in glob.glob(os.path.join(ROOT, "include", "*.h")))
+    for name, (_, args) in _lib.SIGNATURES.items():
+        m = re.search(name + r"\s*\(([^;]*)\);", src, re.S)
+        assert m, name
+        assert len([a for a in m.group(1).split(",") if a.strip()]) == len(args), name
+
+
+def test_entry_points_reject_bad_arguments_without_a_gpu():
+    from locals_amd import _lib
+
+    lib = _lib.load()
+    P = ctypes.c_void_p
+    one = P(16)  # never dereferenced: validation fails first
+    # head_dim 64 -> unsupported (-2); null q -> invalid (-1); missing workspace -> -3
+    rc = lib.lcl_qkv_attend(one, 0, one, one, one, one, one, one, 0, None, None, 0.1, 1, 8, 2, 64, 256, 10, 0,
+                            one, one, 1 << 20, None)
+    assert rc == -2
+    rc = lib.lcl_qkv_attend(None, 0, one, one, one, one, one, one, 0, None, None, 0.1, 1, 8, 2, 128, 256, 10, 0,
+                            one, one, 1 << 20, None)
+    assert rc == -1
+    rc = lib.lcl_qkv_attend(one, 0, one, one, one, one, one, one, 0, None, None, 0.1, 1, 8, 2, 128, 256, 10, 0,
+                            one, None, 0, None)
+    assert rc == -3
+    rc = lib.lcl_quantize_append(one, None, 0, one, one, one, None, None, None, 1, 1, 4, 100, 8, 0, 0, None)
+    assert rc == -1  # D not a multiple of 64
+    assert lib.lcl_decode_workspace_bytes(2, 4, 1000, 512) == 2 * 4 * 2 * (2 + 128) * 4
+
+
+def test_python_wrappers_refuse_cpu_tensors():
+    from locals_amd import qkv
+
+    q = torch.zeros(1, 8, 1, 128, dtype=torch.float16)
+    K = qkv._zeros(1, 2, 64, 128, torch.float16)
+    with pytest.raises(ValueError):
+        qkv.attend(q, K, K, 10, None, 0.1, None)
+
+
+def test_create_causal_mask_and_dynamic_roll():
+    from locals_amd import qkv
+
+    m = qkv.create_causal_mask(3, offset=4)
+    assert m.shape == (3, 7) and m[0].tolist() == [True] * 5 + [False] * 2 and m[2].all()
+    mp = qkv.create_causal_mask(2, offset=3, left_padding=torch.tensor([0, 2]))
+    assert mp.shape == (2, 1, 2, 5) and not mp[1, 0, :, :2].any() and mp[0, 0, 1].all()
+    a = torch.arange(10).reshape(2, 1, 5, 1)
+    r = qkv.dynamic_roll(a, torch.tensor([1, 3]))
+    assert r[0, 0, :, 0].tolist() == [4, 0, 1, 2, 3] and r[1, 0, :, 0].tolist() == [7, 8, 9, 5, 6]
+
+
+def _filled(B, H, n, seed):
+    from locals_amd import qkv
+
+    g = torch.Generator().manual_seed(seed)
+    t = qkv._zeros(B, H, n, 128, torch.float16)
+    t[0].copy_(torch.randint(-2 ** 31, 2 ** 31 - 1, t[0].shape, generator=g, dtype=torch.int64).to(torch.int32))
+    t[1].copy_(torch.randn(t[1].shape, generator=g))
+    t[2].copy_(torch.randn(t[2].shape, generator=g))
+    return t
+
+
+def test_batch_cache_merge_extend_filter_extract_on_host():
+    """Row bookkeeping of BatchQuantizedKVCache on CPU buffers: merge left-pads, extend aligns, filter drops the
+    common padding, extract returns a row's own keys."""
+    from locals_amd import qkv
+
+    c1, c2 = qkv.QuantizedKVCache8(), qkv.QuantizedKVCache8()
+    c1.keys, c1.values, c1.offset = _filled(1, 2, 256, 1), _filled(1, 2, 256, 2), 20
+    c2.keys, c2.values, c2.offset = _filled(1, 2, 256, 3), _filled(1, 2, 256, 4), 11
+    b = qkv.QuantizedKVCache8.merge([c1, c2])
+    assert b._idx == 20 and b.left_padding.tolist() == [0, 9] and b.offset.tolist() == [20, 11]
+    for a, x in zip(b.keys, c2.keys):
+        assert torch.equal(a[1, :, 9:20], x[0, :, :11])
+    # extract row 1 = c2's keys exactly
+    e = b.extract(1)
+    assert e.offset == 11 and all(torch.equal(a[0], x[0, :, :11]) for a, x in zip(e.keys, c2.keys))
+    # extend with a longer batch: the shorter side is padded on the left
+    c3 = qkv.QuantizedKVCache8()
+    c3.keys, c3.values, c3.offset = _filled(1, 2, 256, 5), _filled(1, 2, 256, 6), 30
+    b3 = qkv.QuantizedKVCache8.merge([c3])
+    b.extend(b3)
+    assert b._idx == 30 and b.left_padding.tolist() == [10, 19, 0] and b.offset.tolist() == [20, 11, 30]
+    for a, x in zip(b.keys, c1.keys):
+        assert torch.equal(a[0, :, 10:30], x[0, :, :20])
+    # filter rows [0, 1]: their common padding 10 is dropped
+    b.filter([0, 1])
+    assert b._idx == 20 and b.left_padding.tolist() == [0, 9]
+    for a, x in zip(b.keys, c1.keys):
+        assert torch.equal(a[0, :, :20], x[0, :, :20])
+    assert b.nbytes == sum(a.numel() * a.element_size() for a in b.keys + b.values)

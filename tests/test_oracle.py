@@ -1,0 +1,259 @@
+"""Pins the CPU oracle (oracle/) against checks that do not restate it.
+
+Quantizer: hand-derived MLX closed-form groups (tests/golden/quant_known.npz), both tie modes, the
+dequantization error bound, edge-to-code-0, and agreement with the independent C restatement.
+Attention: torch's CPU float64 scaled_dot_product_attention (sink = extra zero key with additive mask) on the
+golden cases and on random ones; invariants of the reference's split-K algebra (block size, key permutation,
+GQA == MHA with repeated K/V, single key, empty range, garbage outside [start, n)).
+Masks: chain tree == causal, the reference's branch formula == ancestor-or-self of the parent array, brute force.
+qk_norm_rope: torch RMS norm + complex RoPE in float64 within the reference's bar 0.02 max|ref|
+(tests/test_flint.py:235-236); v bit-exact.
+"""
+
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import attn as oa
+from oracle import cbind
+from oracle import quant as oq
+
+GOLD = os.path.join(os.path.dirname(__file__), "golden")
+
+
+def _gold(name):
+    return np.load(os.path.join(GOLD, name), allow_pickle=False)
+
+
+# ------------------------------------------------------------------ quantizer
+@pytest.mark.parametrize("mode", ["away", "even"])
+def test_quantize_known_groups(mode):
+    g = _gold("quant_known.npz")
+    w, s, b = oq.quantize(g["x"], round_mode=mode)
+    assert np.array_equal(oq.codes_of(w), g["codes"])
+    assert np.array_equal(s.view(np.uint16), g["scales"].view(np.uint16))
+    assert np.array_equal(b.view(np.uint16), g["biases"].view(np.uint16))
+
+
+def test_quantize_tie_modes():
+    g = _gold("quant_known.npz")
+    assert np.array_equal(oq.codes_of(oq.quantize(g["tie"], round_mode="away")[0]), g["tie_away"])
+    assert np.array_equal(oq.codes_of(oq.quantize(g["tie"], round_mode="even")[0]), g["tie_even"])
+    assert not np.array_equal(g["tie_away"], g["tie_even"])
+
+
+@pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
+@pytest.mark.parametrize("mode", ["away", "even"])
+def test_quantize_error_bound_and_edge(dtype, mode):
+    g = np.random.default_rng(1)
+    x = oq.from_f32((g.standard_normal((500, 128)) * np.exp(g.uniform(-4, 4, (500, 1)))).astype(np.float32), dtype)
+    w, s, b = oq.quantize(x, dtype, round_mode=mode)
+    xf = oq.to_f32(x, dtype).astype(np.float64).reshape(500, 2, 64)
+    c = oq.codes_of(w).astype(np.float64).reshape(500, 2, 64)
+    sf = oq.to_f32(s, dtype).astype(np.float64)[..., None]
+    bf = oq.to_f32(b, dtype).astype(np.float64)[..., None]
+    # the fp32 scale/bias put an interior code within half a step; MLX's zero-point step (scale = edge / q0 with
+    # |q0| >= 128) can push the far extreme at most one step past 255, where it is clamped (1.5 steps).  The
+    # 16-bit rounding of scale and bias adds at most 255 half-ulps of the scale and a half-ulp of the bias.
+    ulp = 2.0 ** (-10 if dtype == "float16" else -7)
+    fp16_terms = 255 * np.abs(sf) * ulp / 2 + np.abs(bf) * ulp / 2 + 1e-30
+    err = np.abs(c * sf + bf - xf)
+    interior = (c > 0) & (c < 255)
+    assert (err <= (np.abs(sf) / 2 * (1 + 1e-5) + fp16_terms) * 1.0001)[interior].all()
+    assert (err <= (np.abs(sf) * 1.5 * (1 + 1e-5) + fp16_terms) * 1.0001).all()
+    # the edge (the extreme of larger magnitude) maps to code 0, the other extreme near 255
+    edge = np.where(np.abs(xf.min(-1)) > np.abs(xf.max(-1)), xf.argmin(-1), xf.argmax(-1))
+    assert (np.take_along_axis(c, edge[..., None], -1) == 0).all()
+    assert (c.max(-1) >= 254).all()
+
+
+@pytest.mark.parametrize("mode", ["away", "even"])
+def test_quantize_numpy_equals_c(mode):
+    g = np.random.default_rng(2)
+    x = (g.standard_normal((3, 7, 50, 128)) * 3).astype(np.float16)
+    a = oq.quantize(x, round_mode=mode)
+    b = cbind.quantize(x, round_mode=mode)
+    for u, v in zip(a, b):
+        assert np.array_equal(u, v)
+
+
+# ------------------------------------------------------------------ attention
+def _sdpa64(q, k, v, scale, vis, sinks):
+    from tests.golden.make_golden import sdpa64
+
+    return sdpa64(q, k, v, scale, vis, sinks)
+
+
+def test_sdpa_golden_cases():
+    g = _gold("attn_sdpa.npz")
+    out = oa.sdpa(g["dec_q"], g["dec_k"], g["dec_v"], 0.0884,
+                  mask=(np.arange(40)[None, None, None, :] >= g["dec_start"][:, None, None, None]),
+                  sinks=g["dec_sinks"])
+    assert np.abs(out - g["dec_out"]).max() < 1e-9
+    out = oa.sdpa(g["cau_q"], g["cau_k"], g["cau_v"], 0.1, mask="causal")
+    assert np.abs(out - g["cau_out"]).max() < 1e-9
+    local = oa.ancestor_mask(g["tree_parents"])
+    out = oa.sdpa(g["tree_q"], g["tree_k"], g["tree_v"], 0.0884, mask=oa.tree_full_mask(local, 9)[None, None],
+                  sinks=g["tree_sinks"])
+    assert np.abs(out - g["tree_out"]).max() < 1e-9
+
+
+def _q8_case(seed, B=3, H=8, KVH=2, cap=300):
+    g = np.random.default_rng(seed)
+    q = g.standard_normal((B, H, 1, 128)).astype(np.float16)
+    K = oq.quantize((g.standard_normal((B, KVH, cap, 128)) * 2).astype(np.float16))
+    V = oq.quantize(g.standard_normal((B, KVH, cap, 128)).astype(np.float16))
+    sinks = (g.standard_normal(H) * 2).astype(np.float16)
+    return g, q, K, V, sinks
+
+
+def test_attend_equals_torch_sdpa_over_dequantized():
+    g, q, K, V, sinks = _q8_case(3)
+    n, start = 257, np.array([0, 13, 200], np.int32)
+    kd, vd = oq.dequantize(*K), oq.dequantize(*V)
+    vis = np.arange(n)[None, None, None, :] >= start[:, None, None, None]
+    ref = _sdpa64(q, kd[:, :, :n], vd[:, :, :n], float(np.float32(0.0884)), vis, sinks.astype(np.float64))
+    assert np.abs(oa.attend(q, K, V, n, sinks, 0.0884, start) - ref).max() < 1e-9
+
+
+def test_attend_invariants():
+    g, q, K, V, sinks = _q8_case(4, B=2)
+    n, start = 290, np.array([0, 31], np.int32)
+    base = oa.attend(q, K, V, n, sinks, 0.0884, start)
+    # key permutation inside each row's range
+    perm = np.arange(K[0].shape[2])
+    perm[31:n] = 31 + g.permutation(n - 31)
+    perm[:31] = g.permutation(31)
+    Kp, Vp = tuple(a[:, :, perm] for a in K), tuple(a[:, :, perm] for a in V)
+    start0 = np.array([0, 31], np.int32)
+    # row 0 sees [0, n): permuting [0,31) and [31,n) separately keeps its key set
+    assert np.abs(oa.attend(q, Kp, Vp, n, sinks, 0.0884, start0) - base).max() < 1e-9
+    # GQA == MHA with K/V repeated G times
+    G = q.shape[1] // K[0].shape[1]
+    Kr, Vr = tuple(np.repeat(a, G, axis=1) for a in K), tuple(np.repeat(a, G, axis=1) for a in V)
+    assert np.abs(oa.attend(q, Kr, Vr, n, sinks, 0.0884, start) - base).max() < 1e-12
+    # sinks = -inf is plain softmax, i.e. torch SDPA without the extra key
+    kd, vd = oq.dequantize(*K), oq.dequantize(*V)
+    vis = np.arange(n)[None, None, None, :] >= start[:, None, None, None]
+    ref = _sdpa64(q, kd[:, :, :n], vd[:, :, :n], float(np.float32(0.0884)), vis, None)
+    assert np.abs(oa.attend(q, K, V, n, None, 0.0884, start) - ref).max() < 1e-9
+    # empty range -> 0; a single key without a sink -> that key's value
+    e = oa.attend(q, K, V, 5, None, 0.0884, np.array([5, 4], np.int32))
+    assert (e[0] == 0).all()
+    assert np.abs(e[1] - vd[1, np.arange(q.shape[1]) // G, 4][:, None]).max() < 1e-12
+
+
+@pytest.mark.parametrize("block", [64, 128, 1024, 0])
+def test_c_split_k_matches_closed_form(block):
+    """The C restatement of qkv.py's two passes equals the float64 closed form for any block size, and ignores
+    NaN/inf garbage outside each row's [start, n)."""
+    g, q, K, V, sinks = _q8_case(5, B=3, H=16, KVH=4, cap=768)
+    n, start = 700, np.array([0, 37, 300], np.int32)
+    ref = oa.attend(q, K, V, n, sinks, 0.0884, start)
+    Kg = (K[0], K[1].copy(), K[2].copy())
+    Kg[1][0, :, n:] = np.float16(np.nan)
+    Kg[2][2, :, :300] = np.float16(np.inf)
+    got = cbind.attend_q8(q, Kg, V, n, sinks, 0.0884, start, block=block)
+    assert np.abs(got - ref).max() < 2e-5
+
+
+def test_causal_alignment_and_chain_tree():
+    # the last query of "causal" sees every key; query i sees N - L + i + 1 keys
+    m = oa.causal_mask(5, 12)
+    assert m[-1].all() and [int(r.sum()) for r in m] == [8, 9, 10, 11, 12]
+    # a chain tree (parents i-1) is the causal mask over the new tokens
+    assert np.array_equal(oa.ancestor_mask(np.arange(-1, 6)), oa.causal_mask(7, 7))
+
+
+def test_branch_mask_is_ancestor_mask():
+    """The reference's formula (locals/treedec.py:56-67): main path then branches laid out contiguously; as a
+    tree, each branch hangs off the last main token."""
+    g = np.random.default_rng(6)
+    for _ in range(20):
+        m = int(g.integers(1, 5))
+        lens = g.integers(1, 4, size=int(g.integers(1, 4)))
+        br = [-1] * m
+        parents = list(range(-1, m - 1))
+        for i, ln in enumerate(lens):
+            for j in range(ln):
+                parents.append(m - 1 if j == 0 else len(br) - 1)
+                br.append(i)
+        assert np.array_equal(oa.branch_mask(br), oa.ancestor_mask(parents))
+
+
+def test_ancestor_mask_brute_force():
+    g = np.random.default_rng(7)
+    for _ in range(20):
+        L = int(g.integers(1, 17))
+        parents = [-1] + [int(g.integers(0, i)) for i in range(1, L)]
+        m = oa.ancestor_mask(parents)
+        for i in range(L):
+            anc = {i}
+            j = parents[i]
+            while j >= 0:
+                anc.add(j)
+                j = parents[j]
+            assert set(np.nonzero(m[i])[0].tolist()) == anc
+
+
+def test_sdpa_random_masks_vs_torch():
+    g = np.random.default_rng(8)
+    q = g.standard_normal((2, 8, 5, 128))
+    k = g.standard_normal((2, 4, 23, 128))
+    v = g.standard_normal((2, 4, 23, 128))
+    vis = g.random((2, 1, 5, 23)) < 0.6
+    vis[..., 0] = True
+    s = g.standard_normal(8)
+    ref = _sdpa64(q, k, v, 0.09, vis, s)
+    assert np.abs(oa.sdpa(q, k, v, 0.09, mask=vis, sinks=s, dtype="float64") - ref).max() < 1e-9
+
+
+def test_ragged_vs_torch():
+    g = np.random.default_rng(9)
+    q = g.standard_normal((4, 8, 128))
+    K = g.standard_normal((3, 2, 50, 128))
+    V = g.standard_normal((3, 2, 50, 128))
+    slots, nkeys = np.array([2, 0, 1, 2]), np.array([50, 1, 0, 17])
+    out = oa.ragged_attention(q, K, V, slots, nkeys, np.array([0.125], np.float32))
+    for r in range(4):
+        if nkeys[r] == 0:
+            assert (out[r] == 0).all()
+            continue
+        kk, vv = K[slots[r]][:, :nkeys[r]][None], V[slots[r]][:, :nkeys[r]][None]
+        ref = _sdpa64(q[r][None, :, None], kk, vv, 0.125, np.ones((1, 1, 1, nkeys[r]), bool), None)
+        assert np.abs(out[r] - ref[0, :, 0]).max() < 1e-9
+
+
+# ------------------------------------------------------------------ qk_norm_rope
+@pytest.mark.parametrize("rope", [True, False])
+@pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
+def test_qk_norm_rope_vs_torch(rope, dtype):
+    g = np.random.default_rng(10)
+    B, L, H, KV, HD = 3, 4, 4, 2, 128
+    x = oq.to_f32(oq.from_f32((g.standard_normal((B, L, (H + 2 * KV) * HD)) * 2).astype(np.float32), dtype), dtype)
+    qw = oq.to_f32(oq.from_f32((1 + 0.05 * g.standard_normal(HD)).astype(np.float32), dtype), dtype)
+    kw = oq.to_f32(oq.from_f32((1 + 0.05 * g.standard_normal(HD)).astype(np.float32), dtype), dtype)
+    offs = np.array([4, 0, 77])
+    q, k, v = oa.qk_norm_rope(x, qw, kw, 1e-6, offs, H, KV, HD, rope, 10000.0, dtype)
+    t = torch.from_numpy(x.astype(np.float64)).reshape(B, L, H + 2 * KV, HD)
+
+    def norm(a, w):
+        return a * torch.rsqrt((a * a).mean(-1, keepdim=True) + 1e-6) * torch.from_numpy(w.astype(np.float64))
+
+    def rot(a):
+        pos = torch.from_numpy(offs)[:, None].double() + torch.arange(L)[None].double()  # (B, L)
+        inv = 10000.0 ** (-torch.arange(HD // 2).double() * 2 / HD)
+        ang = pos[:, :, None, None] * inv  # (B, L, 1, HD/2)
+        z = torch.complex(a[..., :HD // 2], a[..., HD // 2:]) * torch.exp(1j * ang)
+        return torch.cat([z.real, z.imag], -1)
+
+    q0 = norm(t[:, :, :H], qw)
+    k0 = norm(t[:, :, H:H + KV], kw)
+    if rope:
+        q0, k0 = rot(q0), rot(k0)
+    q0, k0 = q0.permute(0, 2, 1, 3).numpy(), k0.permute(0, 2, 1, 3).numpy()
+    assert np.abs(q - q0).max() <= 0.02 * np.abs(q0).max()
+    assert np.abs(k - k0).max() <= 0.02 * np.abs(k0).max()
+    assert np.array_equal(v, x.reshape(B, L, H + 2 * KV, HD)[:, :, H + KV:].transpose(0, 2, 1, 3))
