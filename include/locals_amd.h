@@ -86,6 +86,40 @@ int lcl_quantize_append(const void* k, const void* v, int dt, uint32_t* kw, void
 int lcl_dequantize(const uint32_t* words, const void* scales, const void* biases, int sdt, long long rows, int D,
                    void* out, int odt, void* stream);
 
+/* Bytes of split-K workspace for lcl_sdpa (B rows, H heads, L queries, N keys). */
+size_t lcl_sdpa_workspace_bytes(int B, int H, int L, int N, int block);
+
+/* MLX scaled_dot_product_attention(q, k, v, scale, mask, sinks) as the reference
+ * routes its multi-query variants through it: the 8-bit prefill/span branch of
+ * qkv.attention -> fuse.attend_few over dequantized K/V (locals/qkv.py:270-272,
+ * locals/fuse.py:131-144), tree verification (locals/treedec.py:56-79,
+ * locals/packed.py:107-116) and packed segments (locals/packed.py:137-143).
+ *   q (B, H, L, 128) dtype qdt; out (B, H, L, 128) dtype qdt
+ *   kvfmt 0: 8-bit triples kw/ks/kb, vw/vs/vb as in lcl_qkv_attend (scales dtype kvdt)
+ *   kvfmt 1: 16-bit kf, vf (B, KVH, cap, 128) dtype kvdt
+ *   the first N <= cap keys of each buffer row are attended; start (B,) or NULL
+ *   masks keys before start[b] (left padding)
+ *   mask_kind 0 none; 1 causal (query i sees key j iff j <= N - L + i);
+ *   2 tree: key j < N - L visible to all, key N - L + d visible to query i iff
+ *     bit d of tree[b * tree_bs + i] (L <= 64; tree_bs = L, or 0 for one shared mask);
+ *   3 dense: uint8 dense[b*msb + h*msh + i*msq + j*msk] != 0 (strides may be 0)
+ *   sinks (H,) float32 or NULL.  A query with no visible key and no sink gives 0. */
+int lcl_sdpa(const void* q, int qdt, int kvfmt, const uint32_t* kw, const void* ks, const void* kb,
+             const uint32_t* vw, const void* vs, const void* vb, const void* kf, const void* vf, int kvdt,
+             const int32_t* start, int mask_kind, const unsigned long long* tree, long long tree_bs,
+             const uint8_t* dense, long long msb, long long msh, long long msq, long long msk, const float* sinks,
+             float scale, int B, int H, int KVH, int L, int N, int head_dim, int cap, int block, void* out,
+             void* workspace, size_t workspace_bytes, void* stream);
+
+/* Profiling form of lcl_sdpa: pass 1's dispatch bracketed by two hipEvent_t.  No
+ * counterpart in the reference. */
+int lcl_sdpa_ex(const void* q, int qdt, int kvfmt, const uint32_t* kw, const void* ks, const void* kb,
+                const uint32_t* vw, const void* vs, const void* vb, const void* kf, const void* vf, int kvdt,
+                const int32_t* start, int mask_kind, const unsigned long long* tree, long long tree_bs,
+                const uint8_t* dense, long long msb, long long msh, long long msq, long long msk, const float* sinks,
+                float scale, int B, int H, int KVH, int L, int N, int head_dim, int cap, int block, void* out,
+                void* workspace, size_t workspace_bytes, void* stream, void* ev_start, void* ev_stop);
+
 #ifdef __cplusplus
 }
 #endif

@@ -23,6 +23,7 @@ P = ctypes.c_void_p
 I = ctypes.c_int
 F = ctypes.c_float
 Z = ctypes.c_size_t
+LL = ctypes.c_longlong
 
 # name -> (restype, argtypes); must match include/locals_amd.h
 SIGNATURES = {
@@ -32,6 +33,11 @@ SIGNATURES = {
     "lcl_ragged_attention": (I, [P, I, P, P, I, P, P, F, P, I, I, I, I, I, I, I, P, P, Z, P]),
     "lcl_quantize_append": (I, [P, P, I, P, P, P, P, P, P, I, I, I, I, I, I, I, P]),
     "lcl_dequantize": (I, [P, P, P, I, ctypes.c_longlong, I, P, I, P]),
+    "lcl_sdpa_workspace_bytes": (Z, [I, I, I, I, I]),
+    "lcl_sdpa": (I, [P, I, I, P, P, P, P, P, P, P, P, I, P, I, P, LL, P, LL, LL, LL, LL, P, F, I, I, I, I, I, I, I, I,
+                     P, P, Z, P]),
+    "lcl_sdpa_ex": (I, [P, I, I, P, P, P, P, P, P, P, P, I, P, I, P, LL, P, LL, LL, LL, LL, P, F, I, I, I, I, I, I, I,
+                        I, P, P, Z, P, P, P]),
 }
 
 _lib = None

@@ -129,12 +129,16 @@ def sdpa(q, k, v, scale: float, mask=None, sinks=None, dtype: str = "float16") -
     return out
 
 
-def sdpa_q8(q, keys, values, scale: float, mask=None, sinks=None, n: int | None = None, dtype: str = "float16"):
+def sdpa_q8(q, keys, values, scale: float, mask=None, sinks=None, n: int | None = None, dtype: str = "float16",
+            round_kv: bool = True):
     """``attend_few(q, dequantized(K), dequantized(V), ...)`` (locals/qkv.py:270-272): SDPA over the first
-    ``n`` keys of 8-bit triples.  The reference dequantizes into T before MLX's attention; this closed form
-    uses the exact float64 dequantization (the T rounding is within the tolerance)."""
-    kd = dequantize(*keys, dtype=dtype)
-    vd = dequantize(*values, dtype=dtype)
+    ``n`` keys of 8-bit triples.  The reference dequantizes into T (``mx.dequantize`` returns the scales' dtype)
+    before MLX's attention; ``round_kv`` rounds the fp32 dequantized values to T likewise."""
+    kd = dequantize(*keys, dtype=dtype, out=np.float32 if round_kv else np.float64)
+    vd = dequantize(*values, dtype=dtype, out=np.float32 if round_kv else np.float64)
+    if round_kv:
+        kd = _round_t(kd, dtype).astype(np.float64)
+        vd = _round_t(vd, dtype).astype(np.float64)
     if n is not None:
         kd, vd = kd[:, :, :n], vd[:, :, :n]
     sk = None if sinks is None else _f64(sinks, dtype)

@@ -38,7 +38,7 @@ def test_signature_arity_matches_header():
 
     src = "".join(open(h).read() for h in glob.glob(os.path.join(ROOT, "include", "*.h")))
     for name, (_, args) in _lib.SIGNATURES.items():
-        m = re.search(name + r"\s*\(([^;]*)\);", src, re.S)
+        m = re.search(r"(?:int|size_t|void)\s+" + name + r"\s*\(([^;]*)\);", src, re.S)
         assert m, name
         assert len([a for a in m.group(1).split(",") if a.strip()]) == len(args), name
 

@@ -1,0 +1,195 @@
+"""GPU parity of lcl_sdpa (multi-query masked attention, split-K on MFMA) against the float64 oracle.
+
+Cases: the chunked-prefill shape (causal over an 8-bit prefix, the last query aligned with the last key,
+locals/fuse.py:131-137), tree verification (prefix visible, ancestor-only among the new tokens,
+locals/treedec.py:56-67), dense boolean masks (locals/fuse.py:139), sinks, left padding, fp16 and bf16, and the
+reference's invariants: a chunk equals decoding its tokens one by one (tests/test_flint.py:420-455), a chain tree
+equals the causal mask, 5 to 8 queries unpadded equal the reference's padded pass (tests/test_flint.py:534-552).
+Bars: 2e-3 max-abs for fp16 outputs; bf16 2^-7 (1 + max|ref|) (tests/test_flint.py:295).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import attn as oa
+from oracle import quant as oq
+from tests.inputs import normal16, q8_cache, rng, to_torch, triple_to_torch
+
+pytestmark = pytest.mark.gpu
+
+
+def _np(t):
+    return t.float().cpu().numpy().astype(np.float64)
+
+
+def _tol(ref, dtype):
+    return 2e-3 if dtype == "float16" else 2 ** -7 * (1 + np.abs(ref).max())
+
+
+@pytest.mark.parametrize("H,KVH,L,N", [(32, 8, 64, 600), (16, 8, 37, 300), (4, 2, 9, 9), (8, 8, 130, 1100),
+                                       (32, 4, 16, 2100)])
+def test_causal_prefill_q8(dev, H, KVH, L, N):
+    from locals_amd.sdpa import scaled_dot_product_attention
+
+    print(f"causal q8 H={H} KVH={KVH} L={L} N={N}", flush=True)
+    g = rng(100 + H + L + N)
+    B, cap = 2, (N + 255) // 256 * 256
+    q = normal16(g, (B, H, L, 128))
+    K, V = q8_cache(g, B, KVH, cap, kscale=2.0)
+    sinks = normal16(g, (H,), 2.0)
+    Kt, Vt = triple_to_torch(K, dev), triple_to_torch(V, dev)
+    got = scaled_dot_product_attention(to_torch(q, dev), tuple(a[:, :, :N] for a in Kt),
+                                       tuple(a[:, :, :N] for a in Vt), scale=0.0884, mask="causal",
+                                       sinks=to_torch(sinks, dev))
+    torch.cuda.synchronize()
+    ref = oa.sdpa_q8(q, K, V, 0.0884, "causal", sinks, n=N)
+    assert np.abs(_np(got) - ref).max() <= 2e-3
+
+
+@pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
+def test_tree_verify_q8(dev, dtype):
+    from locals_amd.sdpa import TreeMask, scaled_dot_product_attention
+
+    g = rng(7)
+    B, H, KVH, L, P = 3, 32, 8, 16, 500
+    N, cap = P + L, 768
+    q = normal16(g, (B, H, L, 128), dtype=dtype)
+    K, V = q8_cache(g, B, KVH, cap, dtype=dtype)
+    parents = [[-1] + [int(g.integers(max(0, i - 3), i)) for i in range(1, L)] for _ in range(B)]
+    local = np.stack([oa.ancestor_mask(pp) for pp in parents])
+    tm = TreeMask.from_local(torch.from_numpy(local), device=dev)
+    Kt, Vt = triple_to_torch(K, dev, dtype), triple_to_torch(V, dev, dtype)
+    got = scaled_dot_product_attention(to_torch(q, dev, dtype), tuple(a[:, :, :N] for a in Kt),
+                                       tuple(a[:, :, :N] for a in Vt), scale=0.0884, mask=tm)
+    torch.cuda.synchronize()
+    vis = np.stack([oa.tree_full_mask(m, P) for m in local])[:, None]
+    ref = oa.sdpa_q8(q, K, V, 0.0884, vis, None, n=N, dtype=dtype)
+    assert np.abs(_np(got) - ref).max() <= _tol(ref, dtype)
+
+
+@pytest.mark.parametrize("kvdt", ["float16", "bfloat16"])
+@pytest.mark.parametrize("masked", ["causal", "dense", None])
+def test_sdpa_16bit(dev, kvdt, masked):
+    from locals_amd.sdpa import scaled_dot_product_attention
+
+    g = rng(8)
+    B, H, KVH, L, N = 2, 16, 4, 24, 333
+    q = normal16(g, (B, H, L, 128), dtype=kvdt)
+    k = normal16(g, (B, KVH, N, 128), dtype=kvdt)
+    v = normal16(g, (B, KVH, N, 128), dtype=kvdt)
+    sinks = normal16(g, (H,), 1.0, dtype=kvdt)
+    if masked == "dense":
+        vis = g.random((B, 1, L, N)) < 0.5
+        vis[..., 0] = True
+        mask, ref_mask = torch.from_numpy(vis).to(dev), vis
+    else:
+        mask, ref_mask = masked, masked
+    got = scaled_dot_product_attention(to_torch(q, dev, kvdt), to_torch(k, dev, kvdt), to_torch(v, dev, kvdt),
+                                       scale=0.09, mask=mask, sinks=to_torch(sinks, dev, kvdt))
+    torch.cuda.synchronize()
+    f = lambda a: oq.to_f32(a, kvdt)  # noqa: E731
+    ref = oa.sdpa(f(q), f(k), f(v), 0.09, ref_mask, f(sinks), dtype="float64")
+    assert np.abs(_np(got) - ref).max() <= _tol(ref, kvdt)
+
+
+def test_left_padding_start(dev):
+    """start[b] masks the keys before it, like the batch cache's left padding."""
+    from locals_amd.sdpa import scaled_dot_product_attention
+
+    g = rng(9)
+    B, H, KVH, L, N, cap = 3, 8, 2, 5, 200, 256
+    q = normal16(g, (B, H, L, 128))
+    K, V = q8_cache(g, B, KVH, cap)
+    start = np.array([0, 17, 150], np.int32)
+    Kt, Vt = triple_to_torch(K, dev), triple_to_torch(V, dev)
+    got = scaled_dot_product_attention(to_torch(q, dev), tuple(a[:, :, :N] for a in Kt),
+                                       tuple(a[:, :, :N] for a in Vt), scale=0.1, mask="causal",
+                                       start=to_torch(start, dev))
+    torch.cuda.synchronize()
+    vis = oa.causal_mask(L, N)[None, None] & (np.arange(N)[None, None, None, :] >= start[:, None, None, None])
+    ref = oa.sdpa_q8(q, K, V, 0.1, vis, None, n=N)
+    assert np.abs(_np(got) - ref).max() <= 2e-3
+
+
+def test_chunk_equals_tokens_one_by_one(dev):
+    """A causal chunk of L queries equals L one-query passes over the growing prefix (the 8-bit decode kernel)."""
+    from locals_amd import qkv
+    from locals_amd.sdpa import scaled_dot_product_attention
+
+    g = rng(10)
+    B, H, KVH, L, N, cap = 1, 32, 8, 12, 400, 512
+    q = normal16(g, (B, H, L, 128))
+    K, V = q8_cache(g, B, KVH, cap)
+    sinks = normal16(g, (H,), 2.0)
+    Kt, Vt = triple_to_torch(K, dev), triple_to_torch(V, dev)
+    qt, st = to_torch(q, dev), to_torch(sinks, dev)
+    chunk = scaled_dot_product_attention(qt, tuple(a[:, :, :N] for a in Kt), tuple(a[:, :, :N] for a in Vt),
+                                         scale=0.0884, mask="causal", sinks=st)
+    for i in range(L):
+        one = qkv.attend(qt[:, :, i:i + 1].contiguous(), Kt, Vt, N - L + i + 1, st, 0.0884,
+                         torch.zeros(B, dtype=torch.int32, device=dev))
+        torch.cuda.synchronize()
+        assert np.abs(_np(one)[:, :, 0] - _np(chunk)[:, :, i]).max() <= 2e-3
+
+
+def test_chain_tree_is_causal(dev):
+    from locals_amd.sdpa import TreeMask, scaled_dot_product_attention
+
+    g = rng(11)
+    B, H, KVH, L, N = 2, 8, 2, 10, 90
+    q = normal16(g, (B, H, L, 128))
+    k = normal16(g, (B, KVH, N, 128))
+    v = normal16(g, (B, KVH, N, 128))
+    args = (to_torch(q, dev), to_torch(k, dev), to_torch(v, dev))
+    a = scaled_dot_product_attention(*args, scale=0.1, mask="causal")
+    b = scaled_dot_product_attention(*args, scale=0.1, mask=TreeMask.from_parents(list(range(-1, L - 1)), dev))
+    c = scaled_dot_product_attention(*args, scale=0.1, mask=TreeMask.from_branches([-1] * L, dev))
+    torch.cuda.synchronize()
+    assert torch.equal(a, b) and torch.equal(a, c)
+
+
+@pytest.mark.parametrize("L", [5, 6, 7, 8])
+def test_attend_few_five_to_eight(dev, L):
+    """attend_few needs no padding: the real queries get what unpadded MLX attention gives them, under the causal
+    mask, a window mask (2-D and per row), or none (the reference test's cases)."""
+    from locals_amd.fuse import attend_few
+
+    g = rng(20 + L)
+    B, H, KVH, n = 2, 8, 2, 40
+    q = normal16(g, (B, H, L, 128), dtype="bfloat16")
+    k = normal16(g, (B, KVH, n, 128), dtype="bfloat16")
+    v = normal16(g, (B, KVH, n, 128), dtype="bfloat16")
+    sinks = normal16(g, (H,), 1.0, dtype="bfloat16")
+    window = (np.arange(n)[None, :] <= (n - L + np.arange(L))[:, None]) & \
+             (np.arange(n)[None, :] > (n - L + np.arange(L))[:, None] - 9)
+    f = lambda a: oq.to_f32(a, "bfloat16")  # noqa: E731
+    for mask, ref_mask in (("causal", "causal"), (None, None), (torch.from_numpy(window).to(dev), window[None, None]),
+                           (torch.from_numpy(np.broadcast_to(window, (B, 1, L, n)).copy()).to(dev),
+                            np.broadcast_to(window, (B, 1, L, n)))):
+        got = attend_few(to_torch(q, dev, "bfloat16"), to_torch(k, dev, "bfloat16"), to_torch(v, dev, "bfloat16"),
+                         0.09, mask, to_torch(sinks, dev, "bfloat16"))
+        torch.cuda.synchronize()
+        ref = oa.sdpa(f(q), f(k), f(v), 0.09, ref_mask, f(sinks), dtype="float64")
+        assert np.abs(_np(got) - ref).max() <= 1e-2 * (1 + np.abs(ref).max())
+
+
+def test_qkv_attention_prompt_branch(dev):
+    """qkv.attention with L > 1 stores the chunk in the 8-bit cache and attends through the masked kernel."""
+    from locals_amd import qkv
+
+    g = rng(12)
+    B, H, KVH, L0, L = 1, 8, 2, 100, 7
+    cache = qkv.QuantizedKVCache8()
+    k0, v0 = normal16(g, (B, KVH, L0, 128)), normal16(g, (B, KVH, L0, 128))
+    cache.update_and_fetch(to_torch(k0, dev), to_torch(v0, dev))
+    q = normal16(g, (B, H, L, 128))
+    k1, v1 = normal16(g, (B, KVH, L, 128)), normal16(g, (B, KVH, L, 128))
+    sinks = normal16(g, (H,), 1.0)
+    out = qkv.attention(to_torch(q, dev), to_torch(k1, dev), to_torch(v1, dev), cache, 0.0884, "causal",
+                        to_torch(sinks, dev))
+    torch.cuda.synchronize()
+    K = oq.quantize(np.concatenate([k0, k1], 2))
+    V = oq.quantize(np.concatenate([v0, v1], 2))
+    ref = oa.sdpa_q8(q, K, V, 0.0884, "causal", sinks)
+    assert np.abs(_np(out) - ref).max() <= 2e-3
