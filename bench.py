@@ -84,7 +84,116 @@ def config(name: str, seed: int = 0):
         B = 15
         return dict(name="c4d", workload="hybrid batch: the 15 decode rows (BASELINE config 4, decode part)",
                     B=B, H=32, KVH=8, nb=g.integers(2048, 16384, size=B, endpoint=True))
+    if name == "c4":
+        return dict(name="c4", workload="hybrid batch: 512-token causal prefill chunk over a 16,384-token 8-bit "
+                    "prefix + 15 decode rows with contexts U[2k, 16k] (BASELINE config 4)", B=15, H=32, KVH=8,
+                    nb=g.integers(2048, 16384, size=15, endpoint=True), L=512, prefix=16384)
+    if name == "c5":
+        return dict(name="c5", workload="speculative tree verification: 8 rows x 16 draft tokens (random trees, "
+                    "branching 1-3, depth <= 8) over 8,192 cached 8-bit keys (BASELINE config 5)", B=8, H=32, KVH=8,
+                    L=16, prefix=8192)
     raise SystemExit(f"unknown config {name}")
+
+
+def random_tree(g, L=16, max_depth=8):
+    """Preorder parent array of a random tree: each node has 1-3 children while depth <= max_depth."""
+    parents, depth = [-1], [1]
+    frontier = [0]
+    while len(parents) < L and frontier:
+        node = frontier.pop(0)
+        for _ in range(int(g.integers(1, 4))):
+            if len(parents) >= L or depth[node] >= max_depth:
+                break
+            parents.append(node)
+            depth.append(depth[node] + 1)
+            frontier.append(len(parents) - 1)
+    while len(parents) < L:  # chain the rest under the last node that may still grow
+        parents.append(len(parents) - 1)
+        depth.append(depth[-1] + 1)
+    # renumber to preorder
+    children = {i: [] for i in range(L)}
+    for i, p in enumerate(parents[1:], 1):
+        children[p].append(i)
+    order, stack = [], [0]
+    while stack:
+        n = stack.pop()
+        order.append(n)
+        stack.extend(reversed(children[n]))
+    new = {o: i for i, o in enumerate(order)}
+    return [-1 if parents[o] < 0 else new[parents[o]] for o in order]
+
+
+def bench_multi(cfg, args, dev):
+    """C4 (decode rows + causal prefill chunk) and C5 (tree verification): pass-1 times from the dispatch events,
+    FLOPs and bytes from the shapes."""
+    import torch
+
+    from locals_amd import _lib, qkv, sdpa
+
+    lib = _lib.load()
+    stream = _lib.stream_of(dev)
+    H, KVH, L, P = cfg["H"], cfg["KVH"], cfg["L"], cfg["prefix"]
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(4321)
+    Bp = 1 if cfg["name"] == "c4" else cfg["B"]
+    N = P + L
+    cap = (N + 255) // 256 * 256
+    sets = []
+    for s in range(args.sets):
+        K = qkv._zeros(Bp, KVH, cap, 128, torch.float16, dev)
+        V = qkv._zeros(Bp, KVH, cap, 128, torch.float16, dev)
+        for b in range(Bp):
+            kf = torch.randn((1, KVH, cap, 128), generator=gen, device=dev, dtype=torch.float16)
+            vf = torch.randn((1, KVH, cap, 128), generator=gen, device=dev, dtype=torch.float16)
+            qkv.quantize_into(kf, vf, tuple(a[b:b + 1] for a in K), tuple(a[b:b + 1] for a in V), 0)
+        q = torch.randn((Bp, H, L, 128), generator=gen, device=dev, dtype=torch.float16)
+        sets.append((q, K, V))
+    g = np.random.default_rng(7)
+    if cfg["name"] == "c5":
+        trees = [random_tree(g, L) for _ in range(Bp)]
+        local = np.zeros((Bp, L, L), bool)
+        for b, par in enumerate(trees):
+            for i in range(L):
+                j = i
+                while j >= 0:
+                    local[b, i, j] = True
+                    j = par[j]
+        mask = sdpa.TreeMask.from_local(torch.from_numpy(local), device=dev)
+        mk, tree, tree_bs = 2, mask.bits, L
+        pairs = int(Bp * (L * P + local.sum()))
+    else:
+        mk, tree, tree_bs = 1, None, 0
+        pairs = sum(P + i + 1 for i in range(L))
+    flops = pairs * H * 4 * 128
+    kv_bytes = Bp * KVH * N * 272
+    nbytes = int(lib.lcl_sdpa_workspace_bytes(Bp, H, L, N, sdpa.BLOCK))
+    ws = torch.empty(nbytes // 4 + 1, dtype=torch.float32, device=dev)
+    out = torch.empty((Bp, H, L, 128), dtype=torch.float16, device=dev)
+    ev = Events(2 * args.steps + 2)
+    P_ = _lib.ptr
+
+    def run(i, e0=None, e1=None):
+        q, K, V = sets[i % len(sets)]
+        rc = lib.lcl_sdpa_ex(P_(q), 0, 0, P_(K[0]), P_(K[1]), P_(K[2]), P_(V[0]), P_(V[1]), P_(V[2]), None, None, 0,
+                             None, mk, P_(tree), tree_bs, None, 0, 0, 0, 0, None, float(1 / np.sqrt(128)), Bp, H, KVH,
+                             L, N, 128, cap, sdpa.BLOCK, P_(out), P_(ws), nbytes, stream, e0, e1)
+        _lib.check(rc, "lcl_sdpa_ex")
+
+    for i in range(args.warmup):
+        run(i)
+    torch.cuda.synchronize()
+    for i in range(args.steps):
+        run(i, ev.ev[2 * i], ev.ev[2 * i + 1])
+    torch.cuda.synchronize()
+    t = np.array([ev.ms(2 * i, 2 * i + 1) for i in range(args.steps)])
+    ev.close()
+    us = float(t.mean() * 1e3)
+    res = {"kernel": "sdpa_pass1", "L": L, "N": N, "rows": Bp, "avg_us": round(us, 2),
+           "tflops": round(flops / (us * 1e-6) / 1e12, 1), "mfma_frac_of_2.5PF": round(flops / (us * 1e-6) / 2.5e15, 4),
+           "kv_GBs": round(kv_bytes / (us * 1e-6) / 1e9, 1), "flops": flops, "kv_bytes": kv_bytes}
+    if cfg["name"] == "c5":
+        res["trees"] = trees
+    return res
 
 
 def build_sets(cfg, nsets, dev):
@@ -201,6 +310,16 @@ def main():
     cfg = config(args.config)
     if args.block is not None:
         qkv.BLOCK = args.block
+    if cfg["name"] in ("c4", "c5"):
+        from locals_amd import sdpa
+
+        if args.block is not None:
+            sdpa.BLOCK = args.block
+        multi = bench_multi(cfg, args, dev)
+        if cfg["name"] == "c5":
+            print(json.dumps({"config": cfg["workload"], "tree_verify": multi}), flush=True)
+            return
+        cfg = dict(cfg, workload=cfg["workload"])  # the decode rows below; the prefill part reported beside them
     sets, start, n, cap = build_sets(cfg, args.sets, dev)
     B, H, KVH = cfg["B"], cfg["H"], cfg["KVH"]
     lib = _lib.load()
@@ -269,6 +388,9 @@ def main():
                      "traffic": _traffic(cfg["name"])},
         "cpu_baseline": None,
     }
+    if cfg["name"] == "c4":
+        line["prefill"] = multi
+        line["us_per_step_decode_plus_prefill"] = round(ms_step * 1e3 + multi["avg_us"], 2)
     if not args.no_cpu:
         per, reps, threads, cpu, err = cpu_baseline(cfg, sets, start, n, args.cpu_seconds, outs[0])
         line["cpu_baseline"] = {"value": round(b_step / per / 1e9, 3), "unit": "GB/s", "cores": threads,

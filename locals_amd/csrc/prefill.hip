@@ -68,16 +68,29 @@ struct SdpaParams {
   int B, H, KVH, G, L, N, cap, nchunks, chunk, nrowblocks, mask;
 };
 
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef __bf16 b8 __attribute__((ext_vector_type(8)));
+
 template <int MT>
 __device__ __forceinline__ uint16_t to_mt(float x) {
   if constexpr (MT == DT_BF16) return f32_to_bf16_bits(x);
   else return __builtin_bit_cast(uint16_t, _Float16(x));
 }
 
+// two floats -> a packed pair of the MFMA type, round to nearest even
 template <int MT>
-__device__ __forceinline__ f4 mma(uint2 a, uint2 b, f4 c) {
-  if constexpr (MT == DT_BF16) return mfma16bf(pack_s4(a.x, a.y), pack_s4(b.x, b.y), c);
-  else return mfma16(pack_h4(a.x, a.y), pack_h4(b.x, b.y), c);
+__device__ __forceinline__ uint32_t pack2(float a, float b) {
+  if constexpr (MT == DT_BF16) return uint32_t(f32_to_bf16_bits(a)) | (uint32_t(f32_to_bf16_bits(b)) << 16);
+  else return __builtin_bit_cast(uint32_t, h2{_Float16(a), _Float16(b)});
+}
+
+// v_mfma_f32_16x16x32: lane l holds A[l % 16][8 (l / 16) + j], B[8 (l / 16) + j][l % 16], j = 0..7
+template <int MT>
+__device__ __forceinline__ f4 mma32(uint4 a, uint4 b, f4 c) {
+  if constexpr (MT == DT_BF16)
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(b8, a), __builtin_bit_cast(b8, b), c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, a), __builtin_bit_cast(h8, b), c, 0, 0, 0);
 }
 
 template <int DT>
@@ -87,207 +100,351 @@ __device__ __forceinline__ float ldv(const void* p, size_t i) {
   else return f16_bits_to_f32(static_cast<const uint16_t*>(p)[i]);
 }
 
-// key j visible to query i of batch row b and head h (inside the chunk's key range)
-__device__ __forceinline__ bool visible(const SdpaParams& p, int b, int h, int i, int j) {
-  if (p.mask == MK_CAUSAL) return j <= p.N - p.L + i;
-  if (p.mask == MK_TREE) {
-    const int d = j - (p.N - p.L);
-    if (d < 0) return true;
-    return (p.tree[b * p.tree_bs + i] >> d) & 1ull;
-  }
-  if (p.mask == MK_DENSE) return p.dense[b * p.msb + h * p.msh + i * p.msq + j * p.msk] != 0;
-  return true;
+// code pair (1024 + a, 1024 + b) -> scale * code + bias for fp16 scale/bias pairs: exact code, one fp16 rounding
+__device__ __forceinline__ uint32_t dq_h2(uint32_t codes1024, uint32_t sc2, uint32_t bi2) {
+  const h2 c = __builtin_bit_cast(h2, codes1024) - h2{_Float16(1024.0f), _Float16(1024.0f)};
+  return __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, sc2) * c + __builtin_bit_cast(h2, bi2));
 }
 
-// One workgroup: rows [64 rb, 64 rb + 64) of (batch row b, kv head kvh), keys of chunk c.
-// QDT: dtype of q; SDT: dtype of the scales/biases (8-bit) or of K/V (16-bit); MT: MFMA type.
-template <int QDT, int SDT, int FMT, int MT>
+// The raw bytes of one 64-key tile a thread stages (8-bit: codes + its keys' scale/bias; 16-bit: values)
+struct RawTile {
+  u4 k[4];         // K: 8-bit uses k[0..1] (32 codes of key tid/4), 16-bit k[0..3] (32 values)
+  u4 v[4];         // V: 8-bit uses v[k].xy (8 codes of key 4 kq + k), 16-bit v[k] (8 values)
+  uint32_t ks, kb; // K scale / bias (16-bit pair entry of the key's group) -- 8-bit only
+  uint32_t vs[4], vb[4];
+};
+
+// One workgroup: RT x 64 rows of (batch row b, kv head kvh) -- a row is one (query, head) -- and the keys of
+// chunk c.  Per 64-key tile: the next tile's raw bytes are loaded into registers while this tile's MFMAs run,
+// then dequantized into the other LDS buffer (double-buffered, one barrier a tile).
+template <int QDT, int SDT, int FMT, int MT, int MASK, int RT>
 __global__ __launch_bounds__(256) void sdpa_pass1(SdpaParams p) {
   const int c = blockIdx.x, rb = blockIdx.y;
   const int b = blockIdx.z / p.KVH, kvh = blockIdx.z % p.KVH;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, tid = threadIdx.x;
   const int c16 = lane & 15, q4 = lane >> 4;
   const int R = p.L * p.G;
-  const int row0 = 64 * rb;
-  const int wrow = row0 + 16 * wave + c16;  // this lane's row in the S^T / O^T layouts
-  const bool real = wrow < R;
-  const int qi = real ? wrow / p.G : 0, g = real ? wrow % p.G : 0;
-  const int head = kvh * p.G + g;
-  // keys of this chunk any row of the workgroup may see
-  const int last_q = min(R - 1, row0 + 63) / p.G;
-  int klo = max(p.start ? max(p.start[b], 0) : 0, c * p.chunk);
+  const int row0 = 64 * RT * rb;
+  // this lane's rows (one a row tile): r-th tile rows row0 + 64 r + 16 wave + [0, 16)
+  int rowi[RT], qi[RT], head[RT];
+  bool real[RT];
+#pragma unroll
+  for (int r = 0; r < RT; r++) {
+    rowi[r] = row0 + 64 * r + 16 * wave + c16;
+    real[r] = rowi[r] < R;
+    qi[r] = real[r] ? rowi[r] / p.G : 0;
+    head[r] = kvh * p.G + (real[r] ? rowi[r] % p.G : 0);
+  }
+  const int last_q = min(R - 1, row0 + 64 * RT - 1) / p.G;
+  const int slo = p.start ? max(p.start[b], 0) : 0;
+  const int klo = max(slo, c * p.chunk);
   int khi = min(p.N, (c + 1) * p.chunk);
-  if (p.mask == MK_CAUSAL) khi = min(khi, p.N - p.L + last_q + 1);
-  const size_t part_base = (size_t(b) * p.H + head) * p.L + qi;  // (b, h, i) row of the partials
+  if constexpr (MASK == MK_CAUSAL) khi = min(khi, p.N - p.L + last_q + 1);
   if (klo >= khi) {  // uniform: nothing here; rows record an empty part
-    if (real && q4 == 0) {
-      p.pm[part_base * p.nchunks + c] = -INFINITY;
-      p.pl[part_base * p.nchunks + c] = 0.0f;
+    if (q4 == 0) {
+#pragma unroll
+      for (int r = 0; r < RT; r++)
+        if (real[r]) {
+          const size_t part = ((size_t(b) * p.H + head[r]) * p.L + qi[r]) * p.nchunks + c;
+          p.pm[part] = -INFINITY;
+          p.pl[part] = 0.0f;
+        }
     }
     return;
   }
 
-  __shared__ __attribute__((aligned(16))) uint16_t Ks[kKT * kKsStride];
-  __shared__ __attribute__((aligned(16))) uint16_t Vt[kD * kVtStride];
+  __shared__ __attribute__((aligned(16))) uint16_t Ks[2][kKT * kKsStride];
+  __shared__ __attribute__((aligned(16))) uint16_t Vt[2][kD * kVtStride];
 
-  // Q^T as B operands: qb[kk] = q[row c16][16 kk + 4 q4 + i]
-  uint2 qb[8];
-  {
-    const size_t qrow = ((size_t(b) * p.H + head) * p.L + qi) * kD;
+  // Q^T as B operands: qb[r][kk] = q[row][32 kk + 8 q4 + j]
+  uint4 qb[RT][4];
 #pragma unroll
-    for (int kk = 0; kk < 8; kk++) {
-      uint16_t t[4];
+  for (int r = 0; r < RT; r++) {
+    const size_t qrow = ((size_t(b) * p.H + head[r]) * p.L + qi[r]) * kD;
 #pragma unroll
-      for (int i = 0; i < 4; i++) t[i] = to_mt<MT>(real ? ldv<QDT>(p.q, qrow + 16 * kk + 4 * q4 + i) : 0.0f);
-      qb[kk] = make_uint2(t[0] | (uint32_t(t[1]) << 16), t[2] | (uint32_t(t[3]) << 16));
+    for (int kk = 0; kk < 4; kk++) {
+      float x[8];
+#pragma unroll
+      for (int j = 0; j < 8; j++) x[j] = ldv<QDT>(p.q, qrow + 32 * kk + 8 * q4 + j);
+      if (!real[r]) {
+#pragma unroll
+        for (int j = 0; j < 8; j++) x[j] = 0.0f;
+      }
+      qb[r][kk] = make_uint4(pack2<MT>(x[0], x[1]), pack2<MT>(x[2], x[3]), pack2<MT>(x[4], x[5]), pack2<MT>(x[6], x[7]));
     }
   }
 
+  // buffers of this (row, kv head); loads past the capacity read 0
   const size_t tok0 = (size_t(b) * p.KVH + kvh) * p.cap;
-  const int qlim = p.N - p.L + qi;  // causal bound of this lane's row
-  const int slo = p.start ? max(p.start[b], 0) : 0;
+  const uint32_t cap = uint32_t(p.cap);
+  BufRsrc rk, rv, rks, rkb, rvs, rvb;
+  if constexpr (FMT == KV_Q8) {
+    rk = make_rsrc(p.kw + tok0 * 32, cap * 128u);
+    rv = make_rsrc(p.vw + tok0 * 32, cap * 128u);
+    rks = make_rsrc(static_cast<const uint16_t*>(p.ks) + tok0 * 2, cap * 4u);
+    rkb = make_rsrc(static_cast<const uint16_t*>(p.kb) + tok0 * 2, cap * 4u);
+    rvs = make_rsrc(static_cast<const uint16_t*>(p.vs) + tok0 * 2, cap * 4u);
+    rvb = make_rsrc(static_cast<const uint16_t*>(p.vb) + tok0 * 2, cap * 4u);
+  } else {
+    rk = make_rsrc(static_cast<const uint16_t*>(p.kf) + tok0 * kD, cap * 256u);
+    rv = make_rsrc(static_cast<const uint16_t*>(p.vf) + tok0 * kD, cap * 256u);
+  }
+  const int kkey = tid >> 2, kpart = tid & 3;   // K staging: one key, 32 dims
+  const int vkq = tid >> 4, vdq = tid & 15;     // V staging: keys 4 vkq .. +3, dims 8 vdq .. +7
 
-  float m_run = -INFINITY, l_acc = 0.0f;
-  f4 O[8];
-#pragma unroll
-  for (int dd = 0; dd < 8; dd++) O[dd] = f4{0.0f, 0.0f, 0.0f, 0.0f};
-
-  for (int t0 = klo & ~(kKT - 1); t0 < khi; t0 += kKT) {
-    // ---- dequantize / stage the tile: K row-major, V transposed; keys outside [klo, khi) are 0
-    {
-      const int key = tid >> 2, part = tid & 3;  // K: one key, 32 dims
-      const int kg = t0 + key;
-      const bool kin = kg >= klo && kg < khi;
-      const size_t row = tok0 + min(kg, p.cap - 1);
-      uint32_t outw[16];
-      if constexpr (FMT == KV_Q8) {
-        const uint4 c0 = *reinterpret_cast<const uint4*>(p.kw + row * 32 + part * 8);
-        const uint4 c1 = *reinterpret_cast<const uint4*>(p.kw + row * 32 + part * 8 + 4);
-        const float sc = ldv<SDT>(p.ks, row * 2 + (part >> 1)), bi = ldv<SDT>(p.kb, row * 2 + (part >> 1));
-        const uint32_t cw[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
-#pragma unroll
-        for (int w = 0; w < 8; w++) {
-          float v[4];
-#pragma unroll
-          for (int i = 0; i < 4; i++) v[i] = kin ? sc * float((cw[w] >> (8 * i)) & 0xffu) + bi : 0.0f;
-          outw[2 * w] = to_mt<MT>(v[0]) | (uint32_t(to_mt<MT>(v[1])) << 16);
-          outw[2 * w + 1] = to_mt<MT>(v[2]) | (uint32_t(to_mt<MT>(v[3])) << 16);
-        }
-      } else {
-        const uint4* src = reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(p.kf) + row * kD + part * 32);
-#pragma unroll
-        for (int u = 0; u < 4; u++) {
-          const uint4 x = src[u];
-          outw[4 * u] = kin ? x.x : 0u;
-          outw[4 * u + 1] = kin ? x.y : 0u;
-          outw[4 * u + 2] = kin ? x.z : 0u;
-          outw[4 * u + 3] = kin ? x.w : 0u;
-        }
-      }
-      uint4* dst = reinterpret_cast<uint4*>(Ks + key * kKsStride + part * 32);
-#pragma unroll
-      for (int u = 0; u < 4; u++) dst[u] = make_uint4(outw[4 * u], outw[4 * u + 1], outw[4 * u + 2], outw[4 * u + 3]);
-    }
-    {
-      const int kq = tid >> 4, dq = tid & 15;  // V: keys 4 kq .. 4 kq + 3, dims 8 dq .. 8 dq + 7
-      uint16_t v16[4][8];
+  auto load = [&](int t0, RawTile& T) {
+    const uint32_t kk = uint32_t(t0 + kkey);
+    if constexpr (FMT == KV_Q8) {
+      T.k[0] = buf_load_b128(rk, kk * 128u + 32u * kpart, 0);
+      T.k[1] = buf_load_b128(rk, kk * 128u + 32u * kpart, 16);
+      T.ks = buf_load_b32(rks, kk * 4u, 0);
+      T.kb = buf_load_b32(rkb, kk * 4u, 0);
 #pragma unroll
       for (int k = 0; k < 4; k++) {
-        const int kg = t0 + 4 * kq + k;
-        const bool kin = kg >= klo && kg < khi;
-        const size_t row = tok0 + min(kg, p.cap - 1);
-        if constexpr (FMT == KV_Q8) {
-          const uint2 cw = *reinterpret_cast<const uint2*>(p.vw + row * 32 + dq * 2);
-          const float sc = ldv<SDT>(p.vs, row * 2 + (dq >> 3)), bi = ldv<SDT>(p.vb, row * 2 + (dq >> 3));
+        const uint32_t vk = uint32_t(t0 + 4 * vkq + k);
+        const uint32_t lo = buf_load_b32(rv, vk * 128u + 8u * vdq, 0), hi = buf_load_b32(rv, vk * 128u + 8u * vdq, 4);
+        T.v[k] = u4{lo, hi, 0u, 0u};
+        T.vs[k] = buf_load_b32(rvs, vk * 4u, 0);
+        T.vb[k] = buf_load_b32(rvb, vk * 4u, 0);
+      }
+    } else {
 #pragma unroll
-          for (int e = 0; e < 8; e++) {
-            const uint32_t w = e < 4 ? cw.x : cw.y;
-            v16[k][e] = to_mt<MT>(kin ? sc * float((w >> (8 * (e & 3))) & 0xffu) + bi : 0.0f);
+      for (int u = 0; u < 4; u++) T.k[u] = buf_load_b128(rk, kk * 256u + 64u * kpart, 16 * u);
+#pragma unroll
+      for (int k = 0; k < 4; k++) T.v[k] = buf_load_b128(rv, uint32_t(t0 + 4 * vkq + k) * 256u + 16u * vdq, 0);
+    }
+  };
+
+  // dequantize (8-bit) or copy (16-bit) a staged tile into LDS buffer `buf`; keys outside [klo, khi) become 0
+  auto stage = [&](int t0, const RawTile& T, int buf) {
+    {
+      const int kg = t0 + kkey;
+      const bool kin = kg >= klo && kg < khi;
+      uint32_t o[16];
+      if constexpr (FMT == KV_Q8) {
+        const uint32_t cw[8] = {T.k[0].x, T.k[0].y, T.k[0].z, T.k[0].w, T.k[1].x, T.k[1].y, T.k[1].z, T.k[1].w};
+        const int gsel = kpart >> 1;  // group of dims 32 kpart .. + 32
+        if constexpr (MT == DT_F16) {
+          const uint32_t s = (T.ks >> (16 * gsel)) & 0xffffu, bb = (T.kb >> (16 * gsel)) & 0xffffu;
+          const uint32_t s2 = s | (s << 16), b2 = bb | (bb << 16);
+#pragma unroll
+          for (int w = 0; w < 8; w++) {
+            o[2 * w] = dq_h2(codes_to_h2(cw[w], 0x00050004u), s2, b2);
+            o[2 * w + 1] = dq_h2(codes_to_h2(cw[w], 0x00070006u), s2, b2);
           }
         } else {
-          const uint4 x = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(p.vf) + row * kD + dq * 8);
-          const uint32_t xw[4] = {x.x, x.y, x.z, x.w};
+          const float sf = half_of(T.ks, gsel, SDT), bf = half_of(T.kb, gsel, SDT);
 #pragma unroll
-          for (int e = 0; e < 8; e++) v16[k][e] = kin ? uint16_t((xw[e >> 1] >> (16 * (e & 1))) & 0xffffu) : 0;
+          for (int w = 0; w < 8; w++) {
+            o[2 * w] = pack2<MT>(sf * float(cw[w] & 0xffu) + bf, sf * float((cw[w] >> 8) & 0xffu) + bf);
+            o[2 * w + 1] = pack2<MT>(sf * float((cw[w] >> 16) & 0xffu) + bf, sf * float(cw[w] >> 24) + bf);
+          }
+        }
+      } else {
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+          o[4 * u] = T.k[u].x; o[4 * u + 1] = T.k[u].y; o[4 * u + 2] = T.k[u].z; o[4 * u + 3] = T.k[u].w;
         }
       }
+      uint4* dst = reinterpret_cast<uint4*>(&Ks[buf][kkey * kKsStride + kpart * 32]);
 #pragma unroll
-      for (int e = 0; e < 8; e++) {
-        uint2* dst = reinterpret_cast<uint2*>(Vt + (8 * dq + e) * kVtStride + 4 * kq);
-        *dst = make_uint2(v16[0][e] | (uint32_t(v16[1][e]) << 16), v16[2][e] | (uint32_t(v16[3][e]) << 16));
-      }
+      for (int u = 0; u < 4; u++)
+        dst[u] = kin ? make_uint4(o[4 * u], o[4 * u + 1], o[4 * u + 2], o[4 * u + 3]) : make_uint4(0u, 0u, 0u, 0u);
     }
-    __syncthreads();
+    {
+      bool vin[4];
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        const int kg = t0 + 4 * vkq + k;
+        vin[k] = kg >= klo && kg < khi;
+      }
+      uint32_t pr[8][2];  // dims 8 vdq + e: (keys 0,1), (keys 2,3)
+      if constexpr (FMT == KV_Q8) {
+        if constexpr (MT == DT_F16) {
+          const int gsel = vdq >> 3;
+          uint32_t s01, s23, b01, b23;
+          {
+            const uint32_t s0 = (T.vs[0] >> (16 * gsel)) & 0xffffu, s1 = (T.vs[1] >> (16 * gsel)) & 0xffffu;
+            const uint32_t s2 = (T.vs[2] >> (16 * gsel)) & 0xffffu, s3 = (T.vs[3] >> (16 * gsel)) & 0xffffu;
+            const uint32_t b0 = (T.vb[0] >> (16 * gsel)) & 0xffffu, b1 = (T.vb[1] >> (16 * gsel)) & 0xffffu;
+            const uint32_t b2 = (T.vb[2] >> (16 * gsel)) & 0xffffu, b3 = (T.vb[3] >> (16 * gsel)) & 0xffffu;
+            s01 = s0 | (s1 << 16); s23 = s2 | (s3 << 16); b01 = b0 | (b1 << 16); b23 = b2 | (b3 << 16);
+          }
+#pragma unroll
+          for (int h = 0; h < 2; h++) {  // dwords: dims 8 vdq + 4 h .. + 3
+            const uint32_t w0 = h ? T.v[0].y : T.v[0].x, w1 = h ? T.v[1].y : T.v[1].x;
+            const uint32_t w2 = h ? T.v[2].y : T.v[2].x, w3 = h ? T.v[3].y : T.v[3].x;
+            const uint32_t x01 = __builtin_amdgcn_perm(w1, w0, 0x05010400u), y01 = __builtin_amdgcn_perm(w1, w0, 0x07030602u);
+            const uint32_t x23 = __builtin_amdgcn_perm(w3, w2, 0x05010400u), y23 = __builtin_amdgcn_perm(w3, w2, 0x07030602u);
+            pr[4 * h + 0][0] = dq_h2(codes_to_h2(x01, 0x00050004u), s01, b01);
+            pr[4 * h + 1][0] = dq_h2(codes_to_h2(x01, 0x00070006u), s01, b01);
+            pr[4 * h + 2][0] = dq_h2(codes_to_h2(y01, 0x00050004u), s01, b01);
+            pr[4 * h + 3][0] = dq_h2(codes_to_h2(y01, 0x00070006u), s01, b01);
+            pr[4 * h + 0][1] = dq_h2(codes_to_h2(x23, 0x00050004u), s23, b23);
+            pr[4 * h + 1][1] = dq_h2(codes_to_h2(x23, 0x00070006u), s23, b23);
+            pr[4 * h + 2][1] = dq_h2(codes_to_h2(y23, 0x00050004u), s23, b23);
+            pr[4 * h + 3][1] = dq_h2(codes_to_h2(y23, 0x00070006u), s23, b23);
+          }
+        } else {
+          const int gsel = vdq >> 3;
+          float sf[4], bf[4];
+#pragma unroll
+          for (int k = 0; k < 4; k++) {
+            sf[k] = half_of(T.vs[k], gsel, SDT);
+            bf[k] = half_of(T.vb[k], gsel, SDT);
+          }
+#pragma unroll
+          for (int e = 0; e < 8; e++) {
+            float v[4];
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+              const uint32_t w = e < 4 ? T.v[k].x : T.v[k].y;
+              v[k] = sf[k] * float((w >> (8 * (e & 3))) & 0xffu) + bf[k];
+            }
+            pr[e][0] = pack2<MT>(v[0], v[1]);
+            pr[e][1] = pack2<MT>(v[2], v[3]);
+          }
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+          const int u = e >> 1;
+          const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
+          const uint32_t w0 = u == 0 ? T.v[0].x : u == 1 ? T.v[0].y : u == 2 ? T.v[0].z : T.v[0].w;
+          const uint32_t w1 = u == 0 ? T.v[1].x : u == 1 ? T.v[1].y : u == 2 ? T.v[1].z : T.v[1].w;
+          const uint32_t w2 = u == 0 ? T.v[2].x : u == 1 ? T.v[2].y : u == 2 ? T.v[2].z : T.v[2].w;
+          const uint32_t w3 = u == 0 ? T.v[3].x : u == 1 ? T.v[3].y : u == 2 ? T.v[3].z : T.v[3].w;
+          pr[e][0] = __builtin_amdgcn_perm(w1, w0, sel);
+          pr[e][1] = __builtin_amdgcn_perm(w3, w2, sel);
+        }
+      }
+      const uint32_t m01 = (vin[0] ? 0xffffu : 0u) | (vin[1] ? 0xffff0000u : 0u);
+      const uint32_t m23 = (vin[2] ? 0xffffu : 0u) | (vin[3] ? 0xffff0000u : 0u);
+#pragma unroll
+      for (int e = 0; e < 8; e++)
+        *reinterpret_cast<uint2*>(&Vt[buf][(8 * vdq + e) * kVtStride + 4 * vkq]) =
+            make_uint2(pr[e][0] & m01, pr[e][1] & m23);
+    }
+  };
 
-    // ---- S^T = K Q^T for this wave's 16 rows: st[t][i] = S[row c16][key t0 + 16 t + 4 q4 + i]
-    f4 st[4];
+  float m_run[RT], l_acc[RT];
+  f4 O[RT][8];
 #pragma unroll
-    for (int t = 0; t < 4; t++) {
-      f4 a = f4{0.0f, 0.0f, 0.0f, 0.0f};
-      const uint16_t* krow = Ks + (16 * t + c16) * kKsStride + 4 * q4;
+  for (int r = 0; r < RT; r++) {
+    m_run[r] = -INFINITY;
+    l_acc[r] = 0.0f;
 #pragma unroll
-      for (int kk = 0; kk < 8; kk++) a = mma<MT>(*reinterpret_cast<const uint2*>(krow + 16 * kk), qb[kk], a);
-      st[t] = a;
-    }
-    // ---- mask, base-2 logits, running max
-    float tmax = -INFINITY;
+    for (int dd = 0; dd < 8; dd++) O[r][dd] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+  }
+  // per-row mask state
+  unsigned long long tbits[RT];
+  const uint8_t* drow[RT];
 #pragma unroll
-    for (int t = 0; t < 4; t++) {
-#pragma unroll
-      for (int i = 0; i < 4; i++) {
-        const int j = t0 + 16 * t + 4 * q4 + i;
-        bool ok = real && j >= klo && j < khi && j >= slo;
-        if (p.mask == MK_CAUSAL) ok = ok && j <= qlim;
-        else if (p.mask != MK_NONE) ok = ok && visible(p, b, head, qi, j);
-        const float s = ok ? st[t][i] * p.scale_log2 : -INFINITY;
-        st[t][i] = s;
-        tmax = fmaxf(tmax, s);
-      }
-    }
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
-    if (tmax > m_run + kThr) {  // per-lane (row) rescale: O^T rows are lane-local
-      const float corr = m_run == -INFINITY ? 0.0f : fast_exp2(m_run - tmax);
-      m_run = tmax;
-      l_acc *= corr;
-#pragma unroll
-      for (int dd = 0; dd < 8; dd++) O[dd] *= corr;
-    }
-    // ---- P (rounded to the MFMA type) and O^T += V^T P^T
-    uint2 pb[4];
-#pragma unroll
-    for (int t = 0; t < 4; t++) {
-      float pv[4];
-#pragma unroll
-      for (int i = 0; i < 4; i++) {
-        pv[i] = st[t][i] == -INFINITY ? 0.0f : fast_exp2(st[t][i] - m_run);
-        l_acc += pv[i];
-      }
-      pb[t] = make_uint2(to_mt<MT>(pv[0]) | (uint32_t(to_mt<MT>(pv[1])) << 16),
-                         to_mt<MT>(pv[2]) | (uint32_t(to_mt<MT>(pv[3])) << 16));
-    }
-#pragma unroll
-    for (int dd = 0; dd < 8; dd++) {
-      const uint16_t* vrow = Vt + (16 * dd + c16) * kVtStride + 4 * q4;
-#pragma unroll
-      for (int t = 0; t < 4; t++) O[dd] = mma<MT>(*reinterpret_cast<const uint2*>(vrow + 16 * t), pb[t], O[dd]);
-    }
-    __syncthreads();
+  for (int r = 0; r < RT; r++) {
+    tbits[r] = 0ull;
+    drow[r] = nullptr;
+    if constexpr (MASK == MK_TREE) tbits[r] = real[r] ? p.tree[b * p.tree_bs + qi[r]] : 0ull;
+    if constexpr (MASK == MK_DENSE) drow[r] = p.dense + b * p.msb + head[r] * p.msh + qi[r] * p.msq;
   }
 
-  // ---- the row's part: m, l (summed over the 4 lanes of the row), o[dims]
-  l_acc += __shfl_xor(l_acc, 16);
-  l_acc += __shfl_xor(l_acc, 32);
-  if (!real) return;
-  const size_t part = part_base * p.nchunks + c;
-  if (q4 == 0) {
-    p.pm[part] = m_run;
-    p.pl[part] = l_acc;
-  }
-  if (m_run == -INFINITY) return;
-  float4* po4 = reinterpret_cast<float4*>(p.po + part * kD);
+  auto compute = [&](int t0, int buf) {
 #pragma unroll
-  for (int dd = 0; dd < 8; dd++) po4[4 * dd + q4] = make_float4(O[dd][0], O[dd][1], O[dd][2], O[dd][3]);
+    for (int r = 0; r < RT; r++) {
+      // S^T = K Q^T: st[t][i] = S[row][t0 + 16 t + 4 q4 + i]
+      f4 st[4];
+#pragma unroll
+      for (int t = 0; t < 4; t++) {
+        f4 a = f4{0.0f, 0.0f, 0.0f, 0.0f};
+        const uint16_t* krow = &Ks[buf][(16 * t + c16) * kKsStride + 8 * q4];
+#pragma unroll
+        for (int kk = 0; kk < 4; kk++) a = mma32<MT>(*reinterpret_cast<const uint4*>(krow + 32 * kk), qb[r][kk], a);
+        st[t] = a;
+      }
+      float tmax = -INFINITY;
+#pragma unroll
+      for (int t = 0; t < 4; t++) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          const int j = t0 + 16 * t + 4 * q4 + i;
+          bool ok = real[r] & (j >= klo) & (j < khi);
+          if constexpr (MASK == MK_CAUSAL) ok = ok & (j <= p.N - p.L + qi[r]);
+          if constexpr (MASK == MK_TREE) {
+            const int d = j - (p.N - p.L);
+            ok = ok & ((d < 0) | (((tbits[r] >> (d & 63)) & 1ull) != 0ull));
+          }
+          if constexpr (MASK == MK_DENSE) ok = ok & (drow[r][min(max(j, 0), p.N - 1) * p.msk] != 0);
+          const float s = ok ? st[t][i] * p.scale_log2 : -INFINITY;
+          st[t][i] = s;
+          tmax = fmaxf(tmax, s);
+        }
+      }
+      tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
+      tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+      if (tmax > m_run[r] + kThr) {  // lane-local rescale (O^T rows live in this lane column)
+        const float corr = m_run[r] == -INFINITY ? 0.0f : fast_exp2(m_run[r] - tmax);
+        m_run[r] = tmax;
+        l_acc[r] *= corr;
+#pragma unroll
+        for (int dd = 0; dd < 8; dd++) O[r][dd] *= corr;
+      }
+      uint32_t pw[4][2];
+#pragma unroll
+      for (int t = 0; t < 4; t++) {
+        float pv[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          pv[i] = fast_exp2(st[t][i] - m_run[r]);  // -inf -> 0
+          l_acc[r] += pv[i];
+        }
+        pw[t][0] = pack2<MT>(pv[0], pv[1]);
+        pw[t][1] = pack2<MT>(pv[2], pv[3]);
+      }
+      // O^T += V^T P^T, 32 keys a step: k index 8 q4 + j <-> key 32 u + (j < 4 ? 4 q4 + j : 16 + 4 q4 + j - 4)
+#pragma unroll
+      for (int u = 0; u < 2; u++) {
+        const uint4 pb = make_uint4(pw[2 * u][0], pw[2 * u][1], pw[2 * u + 1][0], pw[2 * u + 1][1]);
+#pragma unroll
+        for (int dd = 0; dd < 8; dd++) {
+          const uint16_t* vrow = &Vt[buf][(16 * dd + c16) * kVtStride + 32 * u + 4 * q4];
+          const uint2 lo = *reinterpret_cast<const uint2*>(vrow), hi = *reinterpret_cast<const uint2*>(vrow + 16);
+          O[r][dd] = mma32<MT>(make_uint4(lo.x, lo.y, hi.x, hi.y), pb, O[r][dd]);
+        }
+      }
+    }
+  };
+
+  const int tfirst = klo & ~(kKT - 1);
+  RawTile A, B;
+  load(tfirst, A);
+  stage(tfirst, A, 0);
+  __syncthreads();
+  int buf = 0;
+  for (int t0 = tfirst; t0 < khi; t0 += kKT) {
+    const bool more = t0 + kKT < khi;
+    if (more) load(t0 + kKT, B);
+    compute(t0, buf);
+    if (more) stage(t0 + kKT, B, buf ^ 1);
+    __syncthreads();
+    buf ^= 1;
+  }
+
+  // ---- each row's part: m, l (summed over the 4 lanes of the row), o[dims]
+#pragma unroll
+  for (int r = 0; r < RT; r++) {
+    float l = l_acc[r];
+    l += __shfl_xor(l, 16);
+    l += __shfl_xor(l, 32);
+    if (!real[r]) continue;
+    const size_t part = ((size_t(b) * p.H + head[r]) * p.L + qi[r]) * p.nchunks + c;
+    if (q4 == 0) {
+      p.pm[part] = m_run[r];
+      p.pl[part] = l;
+    }
+    if (m_run[r] == -INFINITY) continue;
+    float4* po4 = reinterpret_cast<float4*>(p.po + part * kD);
+#pragma unroll
+    for (int dd = 0; dd < 8; dd++) po4[4 * dd + q4] = make_float4(O[r][dd][0], O[r][dd][1], O[r][dd][2], O[r][dd][3]);
+  }
 }
 
 // Join the chunks of each (b, h, i) row with the head's sink; no key and no sink gives 0.
@@ -327,22 +484,34 @@ __global__ __launch_bounds__(256) void sdpa_combine(SdpaCombineParams p) {
   store_from_f32(p.out, size_t(row) * kD + 2 * lane + 1, o1 * inv, p.odt);
 }
 
+template <int QDT, int SDT, int FMT, int MT, int MASK>
+static void launch_rt(int rt, dim3 grid, hipStream_t s, hipEvent_t e0, hipEvent_t e1, const SdpaParams& p) {
+  (void)rt;
+  hipExtLaunchKernelGGL((sdpa_pass1<QDT, SDT, FMT, MT, MASK, 1>), grid, dim3(256), 0, s, e0, e1, 0, p);
+}
+
 template <int QDT, int SDT, int FMT, int MT>
-static void launch_t(dim3 grid, hipStream_t s, hipEvent_t e0, hipEvent_t e1, const SdpaParams& p) {
-  hipExtLaunchKernelGGL((sdpa_pass1<QDT, SDT, FMT, MT>), grid, dim3(256), 0, s, e0, e1, 0, p);
+static void launch_mask(int rt, dim3 grid, hipStream_t s, hipEvent_t e0, hipEvent_t e1, const SdpaParams& p) {
+  switch (p.mask) {
+    case MK_CAUSAL: launch_rt<QDT, SDT, FMT, MT, MK_CAUSAL>(rt, grid, s, e0, e1, p); break;
+    case MK_TREE: launch_rt<QDT, SDT, FMT, MT, MK_TREE>(rt, grid, s, e0, e1, p); break;
+    case MK_DENSE: launch_rt<QDT, SDT, FMT, MT, MK_DENSE>(rt, grid, s, e0, e1, p); break;
+    default: launch_rt<QDT, SDT, FMT, MT, MK_NONE>(rt, grid, s, e0, e1, p); break;
+  }
 }
 
 template <int FMT>
-static void launch_fmt(int qdt, int sdt, dim3 grid, hipStream_t s, hipEvent_t e0, hipEvent_t e1, const SdpaParams& p) {
+static void launch_fmt(int qdt, int sdt, int rt, dim3 grid, hipStream_t s, hipEvent_t e0, hipEvent_t e1,
+                       const SdpaParams& p) {
   // MFMA type: bf16 when the keys/values (or their scales) are bf16, fp16 otherwise
   if (sdt == DT_BF16) {
-    if (qdt == DT_F16) launch_t<DT_F16, DT_BF16, FMT, DT_BF16>(grid, s, e0, e1, p);
-    else if (qdt == DT_BF16) launch_t<DT_BF16, DT_BF16, FMT, DT_BF16>(grid, s, e0, e1, p);
-    else launch_t<DT_F32, DT_BF16, FMT, DT_BF16>(grid, s, e0, e1, p);
+    if (qdt == DT_F16) launch_mask<DT_F16, DT_BF16, FMT, DT_BF16>(rt, grid, s, e0, e1, p);
+    else if (qdt == DT_BF16) launch_mask<DT_BF16, DT_BF16, FMT, DT_BF16>(rt, grid, s, e0, e1, p);
+    else launch_mask<DT_F32, DT_BF16, FMT, DT_BF16>(rt, grid, s, e0, e1, p);
   } else {
-    if (qdt == DT_F16) launch_t<DT_F16, DT_F16, FMT, DT_F16>(grid, s, e0, e1, p);
-    else if (qdt == DT_BF16) launch_t<DT_BF16, DT_F16, FMT, DT_F16>(grid, s, e0, e1, p);
-    else launch_t<DT_F32, DT_F16, FMT, DT_F16>(grid, s, e0, e1, p);
+    if (qdt == DT_F16) launch_mask<DT_F16, DT_F16, FMT, DT_F16>(rt, grid, s, e0, e1, p);
+    else if (qdt == DT_BF16) launch_mask<DT_BF16, DT_F16, FMT, DT_F16>(rt, grid, s, e0, e1, p);
+    else launch_mask<DT_F32, DT_F16, FMT, DT_F16>(rt, grid, s, e0, e1, p);
   }
 }
 
@@ -400,12 +569,16 @@ int lcl_sdpa_ex(const void* q, int qdt, int kvfmt, const uint32_t* kw, const voi
   p.scale_log2 = scale * kLog2e;
   p.B = B; p.H = H; p.KVH = KVH; p.G = H / KVH; p.L = L; p.N = N; p.cap = cap;
   p.nchunks = nchunks; p.chunk = chunk; p.mask = mask_kind;
-  p.nrowblocks = (L * p.G + 63) / 64;
+  // one row tile a wave (64 rows a workgroup): two (128 rows) would reuse each staged tile twice as often but
+  // need ~370 registers a lane (one wave a SIMD), which measured slower
+  const int rows = L * p.G;
+  const int rt = 1;
+  p.nrowblocks = (rows + 64 * rt - 1) / (64 * rt);
   hipEvent_t e0 = static_cast<hipEvent_t>(ev_start), e1 = static_cast<hipEvent_t>(ev_stop);
   {  // with no key in reach every workgroup records empty parts, so the combine needs no cleared workspace
     const dim3 grid(nchunks, p.nrowblocks, B * KVH);
-    if (kvfmt == KV_Q8) launch_fmt<KV_Q8>(qdt, kvdt, grid, stream, e0, e1, p);
-    else launch_fmt<KV_16>(qdt, kvdt, grid, stream, e0, e1, p);
+    if (kvfmt == KV_Q8) launch_fmt<KV_Q8>(qdt, kvdt, rt, grid, stream, e0, e1, p);
+    else launch_fmt<KV_16>(qdt, kvdt, rt, grid, stream, e0, e1, p);
   }
   SdpaCombineParams c{p.pm, p.pl, p.po, sinks, out, B * H * L, H, L, nchunks, qdt};
   hipLaunchKernelGGL(sdpa_combine, dim3((B * H * L + 3) / 4), dim3(256), 0, stream, c);
