@@ -33,6 +33,8 @@
 
 #include <hip/hip_ext.h>
 
+#include <stdlib.h>
+
 #include <type_traits>
 
 #include "lcl_common.h"
@@ -369,6 +371,272 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
   join_waves(p, s_m, s_l, s_o, Gs, r, head0, c);
 }
 
+// ------------------------------------------------- 8-bit pass 1, LDS-staged
+// The workgroup streams its chunk in 64-key blocks through a 3-deep LDS ring filled by
+// direct buffer->LDS loads (whole 128-byte lines per instruction, non-temporal): a block is
+// K codes (8 KB, 16-byte chunks XOR-swizzled by key so operand reads spread over the banks),
+// V codes (8 KB, same swizzle) and the 64 keys' K/V scales and biases (4 x 256 B).  Each wave
+// issues 5 of a block's 20 load instructions; two blocks are in flight while one is computed.
+// Wave w computes the 16-key tile w of each block exactly as the register-fed kernel does,
+// reading its MFMA operands from LDS.  One barrier a block: each wave first waits for its own
+// loads of the block (vmcnt), the barrier then makes every wave's loads visible and frees the
+// slot the next load overwrites.
+constexpr int kBlk = 64;                        // keys a block
+constexpr int kBlkBytes = 8192 + 8192 + 4 * 256; // K codes, V codes, ks/kb/vs/vb
+constexpr int kRing = 3;  // blocks in the ring
+
+__device__ __forceinline__ void lds_load16(BufRsrc r, void* lds, uint32_t voff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)(lds), 16, voff, 0, 0, kNT);
+}
+__device__ __forceinline__ void lds_load4(BufRsrc r, void* lds, uint32_t voff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)(lds), 4, voff, 0, 0, kNT);
+}
+
+template <int QDT, int SDT>
+__global__ __launch_bounds__(256) void qkv_pass1_q8_lds(DecodeParams p) {
+  const int c = blockIdx.x;
+  const int kvh = blockIdx.y / p.nslices, sl = blockIdx.y % p.nslices;
+  const int r = blockIdx.z;
+  int lo, hi;
+  row_range(p.start, p.nkeys, p.n, p.cap, r, lo, hi);
+  const int c0 = c * p.chunk;
+  const int clo = max(lo, c0), chi = min(hi, c0 + p.chunk);
+  if (clo >= chi) return;  // uniform: no key of this row in this chunk
+
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int c16 = lane & 15, q4 = lane >> 4;
+  const int Gs = min(16, p.G - sl * 16);
+  const int head0 = kvh * p.G + sl * 16;
+  const int slot = p.slots ? min(max(p.slots[r], 0), p.kv_rows - 1) : r;
+  const size_t tok0 = (size_t(slot) * p.KVH + kvh) * p.cap;
+  const uint32_t cap = uint32_t(p.cap);
+  const BufRsrc rk = make_rsrc(p.kw + tok0 * 32, cap * 128u);
+  const BufRsrc rv = make_rsrc(p.vw + tok0 * 32, cap * 128u);
+  // the scale/bias array this wave stages: wave 0 K scales, 1 K biases, 2 V scales, 3 V biases
+  const void* sarr = wave == 0 ? p.ks : wave == 1 ? p.kb : wave == 2 ? p.vs : p.vb;
+  const BufRsrc rsw = make_rsrc(static_cast<const uint32_t*>(sarr) + tok0, cap * 4u);
+
+  // three separate LDS objects (not one indexed array) so the compiler can tell a slot being read from the
+  // slots the direct loads are still filling, and waits only for the block it reads; ring0 is also the
+  // 32 KB join buffer after the loop
+  __shared__ __attribute__((aligned(16))) uint8_t ring0[32768];
+  __shared__ __attribute__((aligned(16))) uint8_t ring1[kBlkBytes];
+  __shared__ __attribute__((aligned(16))) uint8_t ring2[kBlkBytes];
+
+  const int b0 = clo & ~(kBlk - 1);                      // first block
+  const int nblk = (chi - 1 - b0) / kBlk + 1;            // blocks of the chunk holding row keys
+  // a block's 20 load instructions: wave w stages K codes 1 KB pieces 2w, 2w + 1, the same V pieces, and
+  // its scale/bias array (256 B).  Code chunk p = 1024 u + 16 lane: key p / 128 ... stored at 16-byte slot
+  // (lane & 7) of its key = chunk ^ (key & 7), so the global chunk read is (lane & 7) ^ (lane >> 3).
+  const uint32_t swz = uint32_t(lane >> 3) * 128u + 16u * uint32_t((lane & 7) ^ (lane >> 3));
+  auto issue = [&](int blk, uint8_t* R) {
+    const uint32_t kb = uint32_t(b0 + blk * kBlk) * 128u;
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+      const int u = 2 * wave + h;
+      lds_load16(rk, R + u * 1024, kb + uint32_t(u) * 1024u + swz);
+      lds_load16(rv, R + 8192 + u * 1024, kb + uint32_t(u) * 1024u + swz);
+    }
+    lds_load4(rsw, R + 16384 + wave * 256, uint32_t(b0 + blk * kBlk + lane) * 4u);
+  };
+
+  // the ring's first two blocks go out first; the query's loads overlap them
+  issue(0, ring0);
+  issue(min(1, nblk - 1), ring1);  // (a repeat of block 0 when there is no second one: the count in flight stays 5 + 5)
+
+  // B operands of Q K^T: qb[4g + jj] = q[head c16][64g + 16q4 + 4jj + i]
+  h4 qb[8];
+  float qs0 = 0.0f, qs1 = 0.0f;
+  {
+    const bool real = c16 < Gs;
+    const size_t qrow = (size_t(r) * p.H + head0 + (real ? c16 : 0)) * kHD;
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      _Float16 t[4];
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        t[i] = _Float16(real ? ld16<QDT>(p.q, qrow + 64 * (j >> 2) + 16 * q4 + 4 * (j & 3) + i) : 0.0f);
+        (j < 4 ? qs0 : qs1) += float(t[i]);
+      }
+      qb[j] = h4{t[0], t[1], t[2], t[3]};
+    }
+  }
+  qs0 += __shfl_xor(qs0, 16);
+  qs0 += __shfl_xor(qs0, 32);
+  qs1 += __shfl_xor(qs1, 16);
+  qs1 += __shfl_xor(qs1, 32);
+  const float C = p.scale_log2;
+  const float zc0 = 1024.0f * qs0 * C, zc1 = 1024.0f * qs1 * C, qc0 = qs0 * C, qc1 = qs1 * C;
+
+  float m_run = -INFINITY, l_acc = 0.0f, wb0 = 0.0f, wb1 = 0.0f;
+  f4 O[8];
+#pragma unroll
+  for (int ii = 0; ii < 8; ii++) O[ii] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+
+  // this wave's tile of a block: keys tb .. tb + 15 with tb = block + 16 wave
+  const int kt = 16 * wave + c16;               // A-operand key within the block
+  const int ks4 = 16 * wave + 4 * q4;           // first of the lane's 4 S/P keys within the block
+  auto compute = [&](int tb, const uint8_t* B, auto masked) {
+    constexpr bool MASKED = decltype(masked)::value;
+    const u4 ka = *reinterpret_cast<const u4*>(B + kt * 128 + 16 * ((q4) ^ (kt & 7)));
+    const u4 kc = *reinterpret_cast<const u4*>(B + kt * 128 + 16 * ((4 + q4) ^ (kt & 7)));
+    const u4 ksc = *reinterpret_cast<const u4*>(B + 16384 + 4 * ks4);
+    const u4 kbi = *reinterpret_cast<const u4*>(B + 16640 + 4 * ks4);
+    const u4 vsc = *reinterpret_cast<const u4*>(B + 16896 + 4 * ks4);
+    const u4 vbi = *reinterpret_cast<const u4*>(B + 17152 + 4 * ks4);
+    uint32_t vd[8];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      const int t = ks4 + k;
+#pragma unroll
+      for (int g = 0; g < 2; g++)
+        vd[2 * k + g] = *reinterpret_cast<const uint32_t*>(B + 8192 + t * 128 + 16 * ((4 * g + (c16 >> 2)) ^ (t & 7)) +
+                                                           4 * (c16 & 3));
+    }
+    f4 a0 = f4{0.0f, 0.0f, 0.0f, 0.0f}, a1 = a0;
+    a0 = mfma16(codes4_to_h4(ka.x), qb[0], a0);
+    a1 = mfma16(codes4_to_h4(kc.x), qb[4], a1);
+    a0 = mfma16(codes4_to_h4(ka.y), qb[1], a0);
+    a1 = mfma16(codes4_to_h4(kc.y), qb[5], a1);
+    a0 = mfma16(codes4_to_h4(ka.z), qb[2], a0);
+    a1 = mfma16(codes4_to_h4(kc.z), qb[6], a1);
+    a0 = mfma16(codes4_to_h4(ka.w), qb[3], a0);
+    a1 = mfma16(codes4_to_h4(kc.w), qb[7], a1);
+    h4 bv[8];
+#pragma unroll
+    for (int g = 0; g < 2; g++) {
+      const uint32_t x01 = __builtin_amdgcn_perm(vd[2 + g], vd[g], 0x05010400u);
+      const uint32_t y01 = __builtin_amdgcn_perm(vd[2 + g], vd[g], 0x07030602u);
+      const uint32_t x23 = __builtin_amdgcn_perm(vd[6 + g], vd[4 + g], 0x05010400u);
+      const uint32_t y23 = __builtin_amdgcn_perm(vd[6 + g], vd[4 + g], 0x07030602u);
+      bv[4 * g + 0] = pack_h4(codes_to_h2(x01, 0x00050004u), codes_to_h2(x23, 0x00050004u));
+      bv[4 * g + 1] = pack_h4(codes_to_h2(x01, 0x00070006u), codes_to_h2(x23, 0x00070006u));
+      bv[4 * g + 2] = pack_h4(codes_to_h2(y01, 0x00050004u), codes_to_h2(y23, 0x00050004u));
+      bv[4 * g + 3] = pack_h4(codes_to_h2(y01, 0x00070006u), codes_to_h2(y23, 0x00070006u));
+    }
+    const uint32_t kscw[4] = {ksc.x, ksc.y, ksc.z, ksc.w}, kbiw[4] = {kbi.x, kbi.y, kbi.z, kbi.w};
+    const uint32_t vscw[4] = {vsc.x, vsc.y, vsc.z, vsc.w}, vbiw[4] = {vbi.x, vbi.y, vbi.z, vbi.w};
+    float s[4];
+    bool valid[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const float u0 = __builtin_fmaf(a0[i], C, -zc0), u1 = __builtin_fmaf(a1[i], C, -zc1);
+      float v = hpart<SDT>(kscw[i], 0) * u0;
+      v = __builtin_fmaf(hpart<SDT>(kscw[i], 1), u1, v);
+      v = __builtin_fmaf(hpart<SDT>(kbiw[i], 0), qc0, v);
+      v = __builtin_fmaf(hpart<SDT>(kbiw[i], 1), qc1, v);
+      if constexpr (MASKED) {
+        const int t = tb + 4 * q4 + i;
+        valid[i] = t >= clo && t < chi;
+        s[i] = valid[i] ? v : -INFINITY;
+      } else {
+        valid[i] = true;
+        s[i] = v;
+      }
+    }
+    float tmax = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+    const bool need = tmax > m_run + kRescaleThr;
+    if (__any(need)) {
+      const float corr = need ? (m_run == -INFINITY ? 0.0f : fast_exp2(m_run - tmax)) : 1.0f;
+      if (need) m_run = tmax;
+      l_acc *= corr;
+      wb0 *= corr;
+      wb1 *= corr;
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const float ci = __shfl(corr, 4 * q4 + i);
+#pragma unroll
+        for (int ii = 0; ii < 8; ii++) O[ii][i] *= ci;
+      }
+    }
+    float w0[4], w1[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      float pr = fast_exp2(s[i] - m_run);
+      float x0 = pr * hpart<SDT>(vscw[i], 0), x1 = pr * hpart<SDT>(vscw[i], 1);
+      float y0 = pr * hpart<SDT>(vbiw[i], 0), y1 = pr * hpart<SDT>(vbiw[i], 1);
+      if constexpr (MASKED) {
+        pr = valid[i] ? pr : 0.0f;
+        x0 = valid[i] ? x0 : 0.0f;
+        x1 = valid[i] ? x1 : 0.0f;
+        y0 = valid[i] ? y0 : 0.0f;
+        y1 = valid[i] ? y1 : 0.0f;
+      }
+      l_acc += pr;
+      w0[i] = x0;
+      w1[i] = x1;
+      wb0 += __builtin_fmaf(-1024.0f, x0, y0);
+      wb1 += __builtin_fmaf(-1024.0f, x1, y1);
+    }
+    uint32_t h0a, l0a, h0b, l0b, h1a, l1a, h1b, l1b;
+    split_h2(w0[0], w0[1], h0a, l0a);
+    split_h2(w0[2], w0[3], h0b, l0b);
+    split_h2(w1[0], w1[1], h1a, l1a);
+    split_h2(w1[2], w1[3], h1b, l1b);
+    const h4 A0h = pack_h4(h0a, h0b), A0l = pack_h4(l0a, l0b);
+    const h4 A1h = pack_h4(h1a, h1b), A1l = pack_h4(l1a, l1b);
+#pragma unroll
+    for (int jj = 0; jj < 4; jj++) {
+      O[jj] = mfma16(A0h, bv[jj], O[jj]);
+      O[4 + jj] = mfma16(A1h, bv[4 + jj], O[4 + jj]);
+    }
+#pragma unroll
+    for (int jj = 0; jj < 4; jj++) {
+      O[jj] = mfma16(A0l, bv[jj], O[jj]);
+      O[4 + jj] = mfma16(A1l, bv[4 + jj], O[4 + jj]);
+    }
+  };
+
+  // block i is read from cur while block i + 2 is loaded into nxt (the slot block i - 1 used)
+  auto step = [&](int i, const uint8_t* cur, uint8_t* nxt) {
+    // own loads of block i done (block i + 1's five remain in flight), then everyone's.  A bare s_barrier:
+    // __syncthreads()'s release fence would wait for every load still filling the ring.  The acquire fence
+    // keeps this step's LDS reads below the barrier.
+    __builtin_amdgcn_s_waitcnt(0x0F75);  // vmcnt(5), expcnt/lgkmcnt untouched
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+    issue(min(i + 2, nblk - 1), nxt);
+    const int tb = b0 + i * kBlk + 16 * wave;
+    if (tb + 16 > clo && tb < chi) {
+      if (tb >= clo && tb + 16 <= chi) compute(tb, cur, std::false_type{});
+      else compute(tb, cur, std::true_type{});
+    }
+  };
+  for (int i = 0; i < nblk; i += kRing) {
+    step(i, ring0, ring2);
+    if (i + 1 >= nblk) break;
+    step(i + 1, ring1, ring0);
+    if (i + 2 >= nblk) break;
+    step(i + 2, ring2, ring1);
+  }
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): no load into the ring outlives the loop
+  __syncthreads();
+
+  // ---- join the 4 waves in LDS (reusing the ring), one part per (row, head, chunk)
+  l_acc += __shfl_xor(l_acc, 16);
+  l_acc += __shfl_xor(l_acc, 32);
+  wb0 += __shfl_xor(wb0, 16);
+  wb0 += __shfl_xor(wb0, 32);
+  wb1 += __shfl_xor(wb1, 16);
+  wb1 += __shfl_xor(wb1, 32);
+  __shared__ float s_m[kWaves][16], s_l[kWaves][16];
+  float (&s_o)[kWaves][16][kHD] = *reinterpret_cast<float (*)[kWaves][16][kHD]>(ring0);
+  if (q4 == 0) {
+    s_m[wave][c16] = m_run;
+    s_l[wave][c16] = l_acc;
+  }
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const float b0v = __shfl(wb0, 4 * q4 + i), b1v = __shfl(wb1, 4 * q4 + i);
+#pragma unroll
+    for (int ii = 0; ii < 8; ii++) s_o[wave][4 * q4 + i][64 * (ii >> 2) + 4 * c16 + (ii & 3)] = O[ii][i] + (ii < 4 ? b0v : b1v);
+  }
+  __syncthreads();
+  join_waves(p, s_m, s_l, s_o, Gs, r, head0, c);
+}
+
 // ------------------------------------------------------------ 16-bit pass 1
 // K/V of dtype KDT (fp16 or bf16) in (rows, KVH, cap, 128).  Q K^T: lane (key
 // c16, quad q4) supplies dims 32q4 + 4j + i of its key for MFMA j; P V: N-tile ii
@@ -602,9 +870,21 @@ __global__ __launch_bounds__(256) void decode_combine(CombineParams p) {
 
 using namespace lcl;
 
+// The register-fed pass 1 is the default (it measured faster at every decode config); LOCALS_AMD_DECODE=lds
+// selects the LDS-staged one.
+static int use_lds_pass1() {
+  static int v = -1;
+  if (v < 0) {
+    const char* e = getenv("LOCALS_AMD_DECODE");
+    v = (e && e[0] == 'l') ? 1 : 0;
+  }
+  return v;
+}
+
 template <int QDT, int SDT>
 static void launch_q8_t(dim3 grid, hipStream_t stream, hipEvent_t e0, hipEvent_t e1, const DecodeParams& p) {
-  hipExtLaunchKernelGGL((qkv_pass1_q8<QDT, SDT>), grid, dim3(256), 0, stream, e0, e1, 0, p);
+  if (use_lds_pass1()) hipExtLaunchKernelGGL((qkv_pass1_q8_lds<QDT, SDT>), grid, dim3(256), 0, stream, e0, e1, 0, p);
+  else hipExtLaunchKernelGGL((qkv_pass1_q8<QDT, SDT>), grid, dim3(256), 0, stream, e0, e1, 0, p);
 }
 
 static void launch_q8(int qdt, int sdt, dim3 grid, hipStream_t stream, hipEvent_t e0, hipEvent_t e1,
