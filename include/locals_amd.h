@@ -120,6 +120,34 @@ int lcl_sdpa_ex(const void* q, int qdt, int kvfmt, const uint32_t* kw, const voi
                 float scale, int B, int H, int KVH, int L, int N, int head_dim, int cap, int block, void* out,
                 void* workspace, size_t workspace_bytes, void* stream, void* ev_start, void* ev_stop);
 
+/* qk_kernel.qk_norm_rope (locals/qk_kernel.py:24-109, metal_kernel source
+ * :24-69, launch :85-109): per-head RMS norms of q and k, RoPE over halves, v
+ * split out.
+ *   qkv  (B, L, (H + 2 KV) * head_dim) dtype dt (f16 or bf16); head_dim 128, 256 or 512
+ *   q_w, k_w (head_dim,) dtype dt: the q_norm / k_norm weights; eps the shared norm eps
+ *   offsets int32 device array: (B,) if offsets_per_row else (1,); position of
+ *     (b, l) is offsets[b or 0] + l
+ *   rope 0: norms only (a layer without RoPE); log2_base = log2(rope base)
+ *   q (B, H, L, head_dim), k and v (B, KV, L, head_dim), dtype dt
+ * Rounding points as qk_kernel.py:56-62: T(w * T(x r)), then T of the rotation;
+ * the angle in fp32 as qk_kernel.py:59; v is copied bit-exactly. */
+int lcl_qk_norm_rope(const void* qkv, int dt, const void* q_w, const void* k_w, const int32_t* offsets,
+                     int offsets_per_row, float eps, float log2_base, int rope, int B, int L, int H, int KV,
+                     int head_dim, void* q, void* k, void* v, void* stream);
+
+/* lcl_qk_norm_rope fused with the 8-bit cache store that follows it
+ * (locals/fuse.py:80-83 -> BatchQuantizedKVCache.update_and_fetch,
+ * locals/qkv.py:309-326): q as lcl_qk_norm_rope; the normed/rotated k and the
+ * raw v are quantized (MLX affine 8 bits, group 64, as lcl_quantize_append, same
+ * round_mode) into positions [prev, prev + L) of the cache triples
+ * kw/vw (B, KV, cap, head_dim/4) uint32, ks/kb/vs/vb (B, KV, cap, head_dim/64)
+ * dtype dt.  The result equals lcl_qk_norm_rope followed by
+ * lcl_quantize_append of its k and v, bit for bit. */
+int lcl_qk_norm_rope_append(const void* qkv, int dt, const void* q_w, const void* k_w, const int32_t* offsets,
+                            int offsets_per_row, float eps, float log2_base, int rope, int B, int L, int H, int KV,
+                            int head_dim, void* q, void* kw, void* ks, void* kb, void* vw, void* vs, void* vb,
+                            int cap, int prev, int round_mode, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

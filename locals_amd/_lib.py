@@ -38,6 +38,8 @@ SIGNATURES = {
                      P, P, Z, P]),
     "lcl_sdpa_ex": (I, [P, I, I, P, P, P, P, P, P, P, P, I, P, I, P, LL, P, LL, LL, LL, LL, P, F, I, I, I, I, I, I, I,
                         I, P, P, Z, P, P, P]),
+    "lcl_qk_norm_rope": (I, [P, I, P, P, P, I, F, F, I, I, I, I, I, I, P, P, P, P]),
+    "lcl_qk_norm_rope_append": (I, [P, I, P, P, P, I, F, F, I, I, I, I, I, I, P, P, P, P, P, P, P, I, I, I, P]),
 }
 
 _lib = None

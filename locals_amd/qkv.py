@@ -183,7 +183,14 @@ def quantized(cache) -> bool:
 def attention(q, k, v, cache, scale: float, mask, sinks) -> torch.Tensor:
     """A layer's attention through a quantized cache (locals/qkv.py:260-272): stores ``k``/``v`` (B, KVH, L, HD),
     then one query a row through ``attend``, a prompt or a tree (several) through the masked 8-bit kernel."""
-    keys, values = cache.update_and_fetch(k, v)
+    cache.update_and_fetch(k, v)
+    return attend_cache(q, cache, scale, mask, sinks)
+
+
+def attend_cache(q, cache, scale: float, mask, sinks) -> torch.Tensor:
+    """The read half of ``attention`` (locals/qkv.py:264-272): ``q`` against a quantized cache that already holds
+    this step's keys and values (written by ``update_and_fetch`` or ``qk_kernel.qk_norm_rope_append``)."""
+    keys, values = cache.keys_and_values() if hasattr(cache, "keys_and_values") else cache.state
     if q.shape[2] == 1 and q.shape[3] == 128:
         start = getattr(cache, "left_padding", None)
         if start is None:
@@ -243,6 +250,20 @@ def dynamic_roll(a: torch.Tensor, shifts: torch.Tensor, axis: int = 2) -> torch.
     return torch.gather(a, axis, idx)
 
 
+def _grow(cache, B: int, H: int, prev: int, S: int, D: int, dtype, device) -> None:
+    """Make ``cache.keys``/``values`` hold prev + S positions: new zeroed buffers of whole ``step``s, the first prev
+    positions copied over (locals/qkv.py:309-319)."""
+    if cache.keys is not None and prev + S <= cache.keys[0].shape[2]:
+        return
+    cap = (prev + S + cache.step - 1) // cache.step * cache.step
+    nk = _zeros(B, H, cap, D, dtype, device)
+    nv = _zeros(B, H, cap, D, dtype, device)
+    if cache.keys is not None:
+        for a, z in zip(cache.keys + cache.values, nk + nv):
+            z[..., :prev, :] = a[..., :prev, :]
+    cache.keys, cache.values = nk, nv
+
+
 class QuantizedKVCache8:
     """mlx-lm's QuantizedKVCache in 8 bits (locals/qkv.py:284-292): one request's (words, scales, biases) buffers
     growing by ``step`` positions; ``merge`` makes a BatchQuantizedKVCache."""
@@ -254,19 +275,19 @@ class QuantizedKVCache8:
         self.keys = self.values = None
         self.offset = 0
 
+    def _reserve(self, B: int, H: int, S: int, D: int, dtype, device) -> int:
+        """Grow the buffers to hold S more positions and advance the offset; returns where the S positions go."""
+        prev = self.offset
+        _grow(self, B, H, prev, S, D, dtype, device)
+        self.offset += S
+        return prev
+
     def update_and_fetch(self, keys: torch.Tensor, values: torch.Tensor):
         B, H, S, D = keys.shape
-        prev = self.offset
-        if self.keys is None or prev + S > self.keys[0].shape[2]:
-            cap = (prev + S + self.step - 1) // self.step * self.step
-            nk = _zeros(B, H, cap, D, keys.dtype, keys.device)
-            nv = _zeros(B, H, cap, values.shape[3], values.dtype, values.device)
-            if self.keys is not None:
-                for a, z in zip(self.keys + self.values, nk + nv):
-                    z[..., :prev, :] = a[..., :prev, :]
-            self.keys, self.values = nk, nv
+        if values.shape != keys.shape:
+            raise ValueError("values must match keys")
+        prev = self._reserve(B, H, S, D, keys.dtype, keys.device)
         quantize_into(keys, values, self.keys, self.values, prev)
-        self.offset += S
         return _slice(self.keys, None, self.offset), _slice(self.values, None, self.offset)
 
     @property
@@ -331,22 +352,23 @@ class BatchQuantizedKVCache:
     def _dev(self):
         return self.left_padding.device
 
-    def update_and_fetch(self, keys: torch.Tensor, values: torch.Tensor):
-        prev, S = self._idx, keys.shape[2]
-        if self.left_padding.device != keys.device:
-            self.left_padding = self.left_padding.to(keys.device)
-            self.offset = self.offset.to(keys.device)
-        if self.keys is None or prev + S > self.keys[0].shape[2]:
-            B, H, _, D = keys.shape
-            cap = (prev + S + self.step - 1) // self.step * self.step
-            nk = _zeros(B, H, cap, D, keys.dtype, keys.device)
-            nv = _zeros(B, H, cap, values.shape[3], values.dtype, values.device)
-            if self.keys is not None:
-                for a, z in zip(self.keys + self.values, nk + nv):
-                    z[..., :prev, :] = a[..., :prev, :]
-            self.keys, self.values = nk, nv
+    def _reserve(self, B: int, H: int, S: int, D: int, dtype, device) -> int:
+        """Grow the buffers to hold S more positions and advance ``offset`` and ``_idx``; returns where the S
+        positions go (the shared buffer index)."""
+        prev = self._idx
+        if self.left_padding.device != device:
+            self.left_padding = self.left_padding.to(device)
+            self.offset = self.offset.to(device)
+        _grow(self, B, H, prev, S, D, dtype, device)
         self.offset = self.offset + S
         self._idx += S
+        return prev
+
+    def update_and_fetch(self, keys: torch.Tensor, values: torch.Tensor):
+        B, H, S, D = keys.shape
+        if values.shape != keys.shape:
+            raise ValueError("values must match keys")
+        prev = self._reserve(B, H, S, D, keys.dtype, keys.device)
         quantize_into(keys, values, self.keys, self.values, prev)
         return self.keys_and_values()
 

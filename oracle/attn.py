@@ -179,9 +179,13 @@ def qk_norm_rope(qkv, q_w, k_w, eps: float, offsets, H: int, KV: int, HD: int, r
     """``qk_kernel.qk_norm_rope`` (locals/qk_kernel.py:24-109) with its rounding points.
 
     qkv (B, L, (H + 2 KV) * HD) as float32 values of ``dtype``; q_w, k_w (HD,) likewise.
-    Per head: r = 1/sqrt(mean(x^2) + eps) (fp32); a = T(w * T(x * r)) (qk_kernel.py:56-57);
-    RoPE over halves at position offsets[b] + l with theta_i = pos * 2^(-2i/HD * log2(base))
-    (qk_kernel.py:51,59-62), rounded to T; v copied exactly (qk_kernel.py:33-37).
+    Per head: r = 1/sqrt(mean(x^2) + eps) with eps the fp32 value the reference passes
+    (qk_kernel.py:50,103); a = T(w * T(x * r)) (qk_kernel.py:56-57); RoPE over halves at
+    position offsets[b] + l (qk_kernel.py:51) with the angle in the reference's fp32 steps
+    (qk_kernel.py:59): e = fp32(-2i) / fp32(HD) * fp32(log2 base), inv = fp32(2^e),
+    theta = fp32(pos * inv); cos/sin of theta and the rotation in float64, rounded to fp32
+    and then to T (qk_kernel.py:60-62); v copied exactly (qk_kernel.py:33-37).
+    Everything else is float64 (sum of squares, r, x * r), rounded to fp32 then T.
     Returns float32 arrays q (B, H, L, HD), k and v (B, KV, L, HD) holding T values.
     """
     x = np.asarray(qkv, dtype=np.float32)
@@ -190,17 +194,18 @@ def qk_norm_rope(qkv, q_w, k_w, eps: float, offsets, H: int, KV: int, HD: int, r
     offs = np.asarray(offsets, dtype=np.int64).reshape(-1)
     qw, kw = np.asarray(q_w, dtype=np.float32), np.asarray(k_w, dtype=np.float32)
     half = HD // 2
-    i = np.arange(half)
-    inv = np.exp2(-(2.0 * i) / HD * np.log2(base))
+    eps32 = float(np.float32(eps))
+    e = (np.float32(-2.0) * np.arange(half, dtype=np.float32)) / np.float32(HD) * np.float32(np.log2(base))
+    inv = np.exp2(e.astype(np.float64)).astype(np.float32)  # (half,) fp32
 
     def norm(t, w):
         ss = (t.astype(np.float64) ** 2).sum(-1, keepdims=True)
-        r = 1.0 / np.sqrt(ss / HD + eps)
+        r = 1.0 / np.sqrt(ss / HD + eps32)
         n = _round_t((t * r).astype(np.float32), dtype)
         return _round_t(w * n, dtype).astype(np.float64)
 
     def rot(a, pos):
-        th = pos[..., None] * inv  # (..., half)
+        th = (pos.astype(np.float32)[..., None] * inv).astype(np.float64)  # fp32 product, (..., half)
         c, s = np.cos(th), np.sin(th)
         lo, hi = a[..., :half], a[..., half:]
         return _round_t(np.concatenate([lo * c - hi * s, lo * s + hi * c], -1).astype(np.float32), dtype)
@@ -209,8 +214,8 @@ def qk_norm_rope(qkv, q_w, k_w, eps: float, offsets, H: int, KV: int, HD: int, r
     kn = norm(x[:, :, H:H + KV], kw)
     pos = (offs[:, None] if offs.size > 1 else np.full((B, 1), offs[0])) + np.arange(L)[None, :]  # (B, L)
     if rope:
-        qn = rot(qn, pos[:, :, None].astype(np.float64))
-        kn = rot(kn, pos[:, :, None].astype(np.float64))
+        qn = rot(qn, pos[:, :, None])
+        kn = rot(kn, pos[:, :, None])
     q = np.asarray(qn, dtype=np.float32).transpose(0, 2, 1, 3)
     k = np.asarray(kn, dtype=np.float32).transpose(0, 2, 1, 3)
     v = x[:, :, H + KV:].transpose(0, 2, 1, 3).copy()

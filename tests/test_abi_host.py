@@ -62,6 +62,21 @@ def test_entry_points_reject_bad_arguments_without_a_gpu():
     rc = lib.lcl_quantize_append(one, None, 0, one, one, one, None, None, None, 1, 1, 4, 100, 8, 0, 0, None)
     assert rc == -1  # D not a multiple of 64
     assert lib.lcl_decode_workspace_bytes(2, 4, 1000, 512) == 2 * 4 * 2 * (2 + 128) * 4
+    # qk_norm_rope: head_dim 64 unsupported; f32 unsupported; null q invalid; H not a multiple of KV invalid;
+    # an empty call (B * L == 0) is a no-op even with null pointers; the fused store past the capacity is invalid
+    qk = lambda qkv, dt, H, KV, hd, B=1, L=1, q=one: lib.lcl_qk_norm_rope(qkv, dt, one, one, one, 0, 1e-6, 13.3, 1, B, L,
+                                                                         H, KV, hd, q, one, one, None)
+    assert qk(one, 0, 4, 2, 64) == -2
+    assert qk(one, 2, 4, 2, 128) == -2
+    assert qk(one, 0, 4, 2, 128, q=None) == -1
+    assert qk(one, 0, 4, 3, 128) == -1
+    assert qk(None, 0, 4, 2, 128, B=0, q=None) == 0
+    rc = lib.lcl_qk_norm_rope_append(one, 0, one, one, one, 0, 1e-6, 13.3, 1, 1, 5, 4, 2, 128, one, one, one, one,
+                                     one, one, one, 256, 254, 0, None)
+    assert rc == -1
+    rc = lib.lcl_qk_norm_rope_append(one, 0, one, one, one, 0, 1e-6, 13.3, 1, 1, 5, 4, 2, 128, one, one, one, one,
+                                     one, one, one, 256, 0, 2, None)
+    assert rc == -1  # round mode
 
 
 def test_python_wrappers_refuse_cpu_tensors():

@@ -229,13 +229,16 @@ def test_ragged_vs_torch():
 # ------------------------------------------------------------------ qk_norm_rope
 @pytest.mark.parametrize("rope", [True, False])
 @pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
-def test_qk_norm_rope_vs_torch(rope, dtype):
+@pytest.mark.parametrize("HD,offs", [(128, [4, 0, 77]), (256, [-3, 1000, 9])])
+def test_qk_norm_rope_vs_torch(rope, dtype, HD, offs):
+    """The oracle against torch's RMS norm and a complex-exponential RoPE in float64: within four rounding steps of
+    T relative to each (lo, hi) pair's size (a dropped term, a swapped half or a wrong sign is O(1) off); v exact."""
     g = np.random.default_rng(10)
-    B, L, H, KV, HD = 3, 4, 4, 2, 128
+    B, L, H, KV = 3, 4, 4, 2
     x = oq.to_f32(oq.from_f32((g.standard_normal((B, L, (H + 2 * KV) * HD)) * 2).astype(np.float32), dtype), dtype)
     qw = oq.to_f32(oq.from_f32((1 + 0.05 * g.standard_normal(HD)).astype(np.float32), dtype), dtype)
     kw = oq.to_f32(oq.from_f32((1 + 0.05 * g.standard_normal(HD)).astype(np.float32), dtype), dtype)
-    offs = np.array([4, 0, 77])
+    offs = np.array(offs)
     q, k, v = oa.qk_norm_rope(x, qw, kw, 1e-6, offs, H, KV, HD, rope, 10000.0, dtype)
     t = torch.from_numpy(x.astype(np.float64)).reshape(B, L, H + 2 * KV, HD)
 
@@ -254,6 +257,28 @@ def test_qk_norm_rope_vs_torch(rope, dtype):
     if rope:
         q0, k0 = rot(q0), rot(k0)
     q0, k0 = q0.permute(0, 2, 1, 3).numpy(), k0.permute(0, 2, 1, 3).numpy()
-    assert np.abs(q - q0).max() <= 0.02 * np.abs(q0).max()
-    assert np.abs(k - k0).max() <= 0.02 * np.abs(k0).max()
+    ulp = 2.0 ** (-11 if dtype == "float16" else -8)
+    for got, ref in ((q, q0), (k, k0)):
+        pair = np.maximum(np.abs(ref[..., :HD // 2]), np.abs(ref[..., HD // 2:]))
+        bound = 4 * ulp * np.concatenate([pair, pair], -1) + 1e-6
+        assert np.all(np.abs(got - ref) <= bound), np.abs(got - ref).max()
     assert np.array_equal(v, x.reshape(B, L, H + 2 * KV, HD)[:, :, H + KV:].transpose(0, 2, 1, 3))
+
+
+def test_qk_norm_rope_position_zero_is_the_norm_and_rope_is_relative():
+    """At position 0 RoPE is the identity; and rotating q and k by the same extra distance leaves q.k unchanged
+    (the angle depends on the position difference only), up to T rounding."""
+    g = np.random.default_rng(11)
+    B, L, H, KV, HD = 1, 1, 2, 1, 128
+    x = oq.to_f32(oq.from_f32((g.standard_normal((B, L, (H + 2 * KV) * HD)) * 2).astype(np.float32), "float16"),
+                  "float16")
+    w = np.ones(HD, np.float32)
+    q0, k0, _ = oa.qk_norm_rope(x, w, w, 1e-6, [0], H, KV, HD, True)
+    qn, kn, _ = oa.qk_norm_rope(x, w, w, 1e-6, [0], H, KV, HD, False)
+    assert np.array_equal(q0, qn) and np.array_equal(k0, kn)
+    dots = []
+    for p in (5, 5 + 64):  # q at p, k at p - 5
+        qp, _, _ = oa.qk_norm_rope(x, w, w, 1e-6, [p], H, KV, HD, True)
+        _, kp, _ = oa.qk_norm_rope(x, w, w, 1e-6, [p - 5], H, KV, HD, True)
+        dots.append(float((qp[0, 0, 0].astype(np.float64) * kp[0, 0, 0]).sum()))
+    assert abs(dots[0] - dots[1]) < 0.05 and abs(dots[0] - float((qn[0, 0, 0] * kn[0, 0, 0]).sum())) > 0.05
