@@ -637,6 +637,329 @@ __global__ __launch_bounds__(256) void qkv_pass1_q8_lds(DecodeParams p) {
   join_waves(p, s_m, s_l, s_o, Gs, r, head0, c);
 }
 
+// ------------------------------------------- 8-bit pass 1 for G <= 4 (quad)
+// With 4 or fewer query heads a kv head, 16 head columns of a 16x16 MFMA are mostly
+// padding, and so is the softmax work done on them.  This pass 1 computes Q K^T on
+// v_mfma_f32_4x4x4_16b_f16 instead: 16 blocks of 4 keys x 4 heads, so a 64-key tile
+// fills every lane with real (key, head) scores:
+//   lane 4b + m holds A_b[m][0..3] (key row m of block b, 4 dims),
+//   lane 4b + n holds B_b[0..3][n] (4 dims of head n) and D_b[0..3][n] (4 keys, head n).
+// Block b = 4 q4 + sigma holds tile keys 16 sigma + 4 q4 + m, chosen so that for the
+// 16-key sub-tile sigma the P V A operand of lane (head n, q4) -- w of keys
+// 16 sigma + 4 q4 + 0..3 -- is exactly what lane 16 q4 + 4 sigma + n computed: one DPP
+// row shift by 4 sigma.  P V stays on 16x16x16 MFMA with the V transposition of the
+// register kernel (rows of heads >= 4 are discarded).
+// Loads: a workgroup is one wave owning one key chunk and its partial.  Each 64-key
+// tile (K codes 8 KB, V codes 8 KB, four 256 B scale/bias arrays) arrives by direct
+// buffer->LDS loads of whole 128-byte lines (20 instructions) into the wave's LDS
+// slot; the wave copies the tile into registers, then sends the next tile's loads into
+// the same slot, so they are in flight while this tile computes and the only loads
+// outstanding at an LDS read are the ones it waits for.  No barrier is needed: a wave
+// only reads what it loaded (vmcnt).  K rows are stored with 16-byte chunk c at slot
+// c ^ hk(key) and V rows at c ^ hv(key), so the 128-bit K reads and the 32-bit V reads
+// are free of bank conflicts.
+constexpr int kQT = 64;                     // keys a tile
+constexpr int kQSlot = 8192 + 8192 + 1024;  // K codes, V codes, ks / kb / vs / vb words
+
+// tile key of QK lane l = 4 b + m (b = 4 q4 + sigma): 16 sigma + 4 q4 + m
+__device__ __forceinline__ int quad_key(int l) { return 16 * ((l >> 2) & 3) + 4 * (l >> 4) + (l & 3); }
+// 16-byte slot swizzles of tile key t's K and V rows
+__device__ __forceinline__ int quad_hk(int t) { return (t & 3) | (((t >> 4) & 1) << 2); }
+__device__ __forceinline__ int quad_hv(int t) { return 4 * ((t >> 2) & 1); }
+
+__device__ __forceinline__ f4 mfma4(h4 a, h4 b, f4 c) { return __builtin_amdgcn_mfma_f32_4x4x4f16(a, b, c, 0, 0, 0); }
+
+// lane i of each 16-lane row takes lane i + SH of the same row (0 past the row's end)
+template <int SH>
+__device__ __forceinline__ uint32_t row_take(uint32_t x) {
+  if constexpr (SH == 0) return x;
+  else return uint32_t(__builtin_amdgcn_update_dpp(0, int(x), 0x100 + SH, 0xf, 0xf, true));
+}
+
+template <int QDT, int SDT>
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void qkv_pass1_q8_quad(DecodeParams p) {
+  const int c = blockIdx.x, kvh = blockIdx.y, r = blockIdx.z;
+  int lo, hi;
+  row_range(p.start, p.nkeys, p.n, p.cap, r, lo, hi);
+  const int c0 = c * p.chunk;
+  const int clo = max(lo, c0), chi = min(hi, c0 + p.chunk);
+  if (clo >= chi) return;  // no key of this row in this chunk
+
+  const int lane = threadIdx.x;
+  const int n = lane & 3;             // QK: head column of this lane
+  const int c16 = lane & 15, q4 = lane >> 4;
+  const int G = p.G;                  // <= 4
+  const int head0 = kvh * G;
+  const int slot = p.slots ? min(max(p.slots[r], 0), p.kv_rows - 1) : r;
+  const size_t tok0 = (size_t(slot) * p.KVH + kvh) * p.cap;
+  const uint32_t cap = uint32_t(p.cap);
+  const BufRsrc rk = make_rsrc(p.kw + tok0 * 32, cap * 128u);
+  const BufRsrc rv = make_rsrc(p.vw + tok0 * 32, cap * 128u);
+  const BufRsrc rks = make_rsrc(static_cast<const uint32_t*>(p.ks) + tok0, cap * 4u);
+  const BufRsrc rkb = make_rsrc(static_cast<const uint32_t*>(p.kb) + tok0, cap * 4u);
+  const BufRsrc rvs = make_rsrc(static_cast<const uint32_t*>(p.vs) + tok0, cap * 4u);
+  const BufRsrc rvb = make_rsrc(static_cast<const uint32_t*>(p.vb) + tok0, cap * 4u);
+
+  __shared__ __attribute__((aligned(16))) uint8_t qtile[kQSlot];
+
+  const int kb0 = clo & ~(kQT - 1);
+  const int ntiles = (chi - 1 - kb0) / kQT + 1;
+  // DMA lane roles: instruction u moves tile keys 8u + (lane >> 3), lane slot (lane & 7)
+  const uint32_t dk_lo = 128u * uint32_t(lane >> 3);
+  const uint32_t dk_c0 = 16u * uint32_t((lane & 7) ^ ((lane >> 3) & 3));        // hk for u with bit 1 clear
+  const uint32_t dk_c1 = 16u * uint32_t((lane & 7) ^ (((lane >> 3) & 3) | 4));  // hk for u with bit 1 set
+  const uint32_t dv_c = 16u * uint32_t((lane & 7) ^ (4 * ((lane >> 5) & 1)));
+  auto issue = [&](int tile, uint8_t* S) {
+    const uint32_t kt = uint32_t(kb0 + tile * kQT);
+#pragma unroll
+    for (int u = 0; u < 8; u++) {
+      const uint32_t row = (kt + 8u * u) * 128u + dk_lo;
+      lds_load16(rk, S + 1024 * u, row + ((u & 2) ? dk_c1 : dk_c0));
+      lds_load16(rv, S + 8192 + 1024 * u, row + dv_c);
+    }
+    const uint32_t so = (kt + uint32_t(lane)) * 4u;
+    lds_load4(rks, S + 16384, so);
+    lds_load4(rkb, S + 16384 + 256, so);
+    lds_load4(rvs, S + 16384 + 512, so);
+    lds_load4(rvb, S + 16384 + 768, so);
+  };
+
+  // the G query rows go to LDS by the same route (rows past G read as 0), then become fp16 in place:
+  // qh[128 n + d] = fp16(q[head n][d]), the B operands of the 4x4x4 products
+  constexpr int QB = QDT == DT_F32 ? 4 : 2;
+  __shared__ __attribute__((aligned(16))) uint8_t qraw[4 * kHD * 4];
+  const BufRsrc rq = make_rsrc(static_cast<const uint8_t*>(p.q) + (size_t(r) * p.H + head0) * kHD * QB,
+                               uint32_t(G * kHD * QB));
+  issue(0, qtile);
+#pragma unroll
+  for (int j = 0; j < 2 * QB; j++) lds_load4(rq, qraw + 256 * j, uint32_t(256 * j + 4 * lane));
+  constexpr int kWaitAll = (0xF << 8) | (0x7 << 4);        // s_waitcnt vmcnt(0)
+  constexpr int kWaitLds = (0x3 << 14) | (0x7 << 4) | 0xF;  // s_waitcnt lgkmcnt(0)
+  __builtin_amdgcn_s_waitcnt(kWaitAll);
+  _Float16* qh = reinterpret_cast<_Float16*>(qraw);
+  float qs0 = 0.0f, qs1 = 0.0f;  // sums of head n's fp16 q over dims [0, 64) and [64, 128)
+  {
+    // lane l converts elements 8 l .. 8 l + 7 (head l / 16, group (l / 8) & 1); all reads precede the writes
+    _Float16 t[8];
+    float part = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      t[i] = _Float16(ld16<QDT>(qraw, size_t(8 * lane + i)));
+      part += float(t[i]);
+    }
+    __builtin_amdgcn_s_waitcnt(kWaitLds);
+#pragma unroll
+    for (int i = 0; i < 8; i++) qh[8 * lane + i] = t[i];
+    part += __shfl_xor(part, 1);
+    part += __shfl_xor(part, 2);
+    part += __shfl_xor(part, 4);
+    // lane 16 h + 8 g holds the sum of head h, group g
+#pragma unroll
+    for (int h = 0; h < 4; h++) {
+      const float g0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(part), 16 * h));
+      const float g1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(part), 16 * h + 8));
+      qs0 = n == h ? g0 : qs0;
+      qs1 = n == h ? g1 : qs1;
+    }
+  }
+  const float C = p.scale_log2;
+  const float zc0 = 1024.0f * qs0 * C, zc1 = 1024.0f * qs1 * C, qc0 = qs0 * C, qc1 = qs1 * C;
+
+  const int tk = quad_key(lane);               // QK row key of this lane
+  const uint32_t krow = 128u * uint32_t(tk);
+  const int hk = quad_hk(tk);
+  const int ts0 = quad_key(lane & ~3);         // first of the 4 keys whose scores this lane holds
+  // P V B operands: lane (c16, q4) reads V words of keys 16 sigma + 4 q4 + k, dims 64 g + 4 c16 .. + 3
+  const uint32_t vcol = 8192u + 64u * uint32_t(q4 & 1) + 4u * uint32_t(c16);
+
+  float m_run = -INFINITY, l_acc = 0.0f, wb0 = 0.0f, wb1 = 0.0f;
+  f4 O[8];
+#pragma unroll
+  for (int ii = 0; ii < 8; ii++) O[ii] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+
+  // the tile as a lane holds it: K chunks of its QK key, the scale words of its 4 score keys, and for each
+  // 16-key sub-tile the V words of keys 16 sigma + 4 q4 + k (dims 64 g + 4 c16 .. + 3) at [sigma][2 k + g]
+  struct QuadTile {
+    u4 k[8];
+    u4 ksc, kbi, vsc, vbi;
+    uint32_t v[4][8];
+  };
+  auto fetch = [&](QuadTile& T) {
+#pragma unroll
+    for (int cc = 0; cc < 8; cc++) T.k[cc] = *reinterpret_cast<const u4*>(qtile + krow + 16 * (cc ^ hk));
+    T.ksc = *reinterpret_cast<const u4*>(qtile + 16384 + 4 * ts0);
+    T.kbi = *reinterpret_cast<const u4*>(qtile + 16640 + 4 * ts0);
+    T.vsc = *reinterpret_cast<const u4*>(qtile + 16896 + 4 * ts0);
+    T.vbi = *reinterpret_cast<const u4*>(qtile + 17152 + 4 * ts0);
+#pragma unroll
+    for (int sg = 0; sg < 4; sg++) {
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        const uint32_t row = 128u * uint32_t(16 * sg + 4 * q4 + k);
+        T.v[sg][2 * k + 0] = *reinterpret_cast<const uint32_t*>(qtile + row + vcol);
+        T.v[sg][2 * k + 1] = *reinterpret_cast<const uint32_t*>(qtile + row + (vcol ^ 64u));
+      }
+    }
+  };
+
+  auto compute = [&](int tile, const QuadTile& T) {
+    const int kt = kb0 + tile * kQT;
+    // ---- S^T = K Q^T, four chains (group g = chunk >> 2, chunk parity)
+    f4 acc[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) acc[i] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int cc = 0; cc < 8; cc++) {
+      const u4 kv = T.k[cc];
+      const u4 qa = *reinterpret_cast<const u4*>(qh + kHD * n + 16 * cc);
+      const u4 qc = *reinterpret_cast<const u4*>(qh + kHD * n + 16 * cc + 8);
+      f4& a = acc[2 * (cc >> 2) + (cc & 1)];
+      a = mfma4(codes4_to_h4(kv.x), pack_h4(qa.x, qa.y), a);
+      a = mfma4(codes4_to_h4(kv.y), pack_h4(qa.z, qa.w), a);
+      a = mfma4(codes4_to_h4(kv.z), pack_h4(qc.x, qc.y), a);
+      a = mfma4(codes4_to_h4(kv.w), pack_h4(qc.z, qc.w), a);
+    }
+    const uint32_t kscw[4] = {T.ksc.x, T.ksc.y, T.ksc.z, T.ksc.w}, kbiw[4] = {T.kbi.x, T.kbi.y, T.kbi.z, T.kbi.w};
+    const uint32_t vscw[4] = {T.vsc.x, T.vsc.y, T.vsc.z, T.vsc.w}, vbiw[4] = {T.vbi.x, T.vbi.y, T.vbi.z, T.vbi.w};
+    // ---- scores of keys ts0 + m for head n (base-2 logits)
+    const bool full = kt >= clo && kt + kQT <= chi;
+    float s[4];
+    bool valid[4];
+#pragma unroll
+    for (int m = 0; m < 4; m++) {
+      const float a0 = acc[0][m] + acc[1][m], a1 = acc[2][m] + acc[3][m];
+      const float u0 = __builtin_fmaf(a0, C, -zc0), u1 = __builtin_fmaf(a1, C, -zc1);
+      float v = hpart<SDT>(kscw[m], 0) * u0;
+      v = __builtin_fmaf(hpart<SDT>(kscw[m], 1), u1, v);
+      v = __builtin_fmaf(hpart<SDT>(kbiw[m], 0), qc0, v);
+      v = __builtin_fmaf(hpart<SDT>(kbiw[m], 1), qc1, v);
+      const int t = kt + ts0 + m;
+      valid[m] = full || (t >= clo && t < chi);
+      s[m] = valid[m] ? v : -INFINITY;
+    }
+    // ---- tile max of head n over the 16 lanes holding it
+    float tmax = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 4));
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 8));
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+    const bool need = tmax > m_run + kRescaleThr;
+    if (__any(need)) {
+      const float corr = need ? (m_run == -INFINITY ? 0.0f : fast_exp2(m_run - tmax)) : 1.0f;
+      if (need) m_run = tmax;
+      l_acc *= corr;
+      wb0 *= corr;
+      wb1 *= corr;
+      // P V rows: lane (c16, q4) register i is head 4 q4 + i; heads 0..3 live in lanes 0..15
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const float ci = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(corr), i));
+#pragma unroll
+        for (int ii = 0; ii < 8; ii++) O[ii][i] *= ci;
+      }
+    }
+    float w0[4], w1[4];
+#pragma unroll
+    for (int m = 0; m < 4; m++) {
+      float pr = fast_exp2(s[m] - m_run);
+      float x0 = pr * hpart<SDT>(vscw[m], 0), x1 = pr * hpart<SDT>(vscw[m], 1);
+      float y0 = pr * hpart<SDT>(vbiw[m], 0), y1 = pr * hpart<SDT>(vbiw[m], 1);
+      // garbage scales of keys outside the range must not reach the sums (0 * inf)
+      pr = valid[m] ? pr : 0.0f;
+      x0 = valid[m] ? x0 : 0.0f;
+      x1 = valid[m] ? x1 : 0.0f;
+      y0 = valid[m] ? y0 : 0.0f;
+      y1 = valid[m] ? y1 : 0.0f;
+      l_acc += pr;
+      w0[m] = x0;
+      w1[m] = x1;
+      wb0 += __builtin_fmaf(-1024.0f, x0, y0);
+      wb1 += __builtin_fmaf(-1024.0f, x1, y1);
+    }
+    uint32_t wh[4], wl[4];  // [g][pair]: fp16 hi / lo of w_g for keys m = 0, 1 and 2, 3
+    split_h2(w0[0], w0[1], wh[0], wl[0]);
+    split_h2(w0[2], w0[3], wh[1], wl[1]);
+    split_h2(w1[0], w1[1], wh[2], wl[2]);
+    split_h2(w1[2], w1[3], wh[3], wl[3]);
+
+    // ---- P V on 16x16x16, one 16-key sub-tile at a time
+    auto pv = [&](auto sig) {
+      constexpr int SG = decltype(sig)::value;
+      const h4 A0h = pack_h4(row_take<4 * SG>(wh[0]), row_take<4 * SG>(wh[1]));
+      const h4 A0l = pack_h4(row_take<4 * SG>(wl[0]), row_take<4 * SG>(wl[1]));
+      const h4 A1h = pack_h4(row_take<4 * SG>(wh[2]), row_take<4 * SG>(wh[3]));
+      const h4 A1l = pack_h4(row_take<4 * SG>(wl[2]), row_take<4 * SG>(wl[3]));
+      const uint32_t (&vd)[8] = T.v[SG];
+      h4 bv[8];
+#pragma unroll
+      for (int g = 0; g < 2; g++) {
+        const uint32_t x01 = __builtin_amdgcn_perm(vd[2 + g], vd[g], 0x05010400u);
+        const uint32_t y01 = __builtin_amdgcn_perm(vd[2 + g], vd[g], 0x07030602u);
+        const uint32_t x23 = __builtin_amdgcn_perm(vd[6 + g], vd[4 + g], 0x05010400u);
+        const uint32_t y23 = __builtin_amdgcn_perm(vd[6 + g], vd[4 + g], 0x07030602u);
+        bv[4 * g + 0] = pack_h4(codes_to_h2(x01, 0x00050004u), codes_to_h2(x23, 0x00050004u));
+        bv[4 * g + 1] = pack_h4(codes_to_h2(x01, 0x00070006u), codes_to_h2(x23, 0x00070006u));
+        bv[4 * g + 2] = pack_h4(codes_to_h2(y01, 0x00050004u), codes_to_h2(y23, 0x00050004u));
+        bv[4 * g + 3] = pack_h4(codes_to_h2(y01, 0x00070006u), codes_to_h2(y23, 0x00070006u));
+      }
+#pragma unroll
+      for (int jj = 0; jj < 4; jj++) {
+        O[jj] = mfma16(A0h, bv[jj], O[jj]);
+        O[4 + jj] = mfma16(A1h, bv[4 + jj], O[4 + jj]);
+      }
+#pragma unroll
+      for (int jj = 0; jj < 4; jj++) {
+        O[jj] = mfma16(A0l, bv[jj], O[jj]);
+        O[4 + jj] = mfma16(A1l, bv[4 + jj], O[4 + jj]);
+      }
+    };
+    pv(std::integral_constant<int, 0>{});
+    pv(std::integral_constant<int, 1>{});
+    pv(std::integral_constant<int, 2>{});
+    pv(std::integral_constant<int, 3>{});
+  };
+
+  for (int tile = 0; tile < ntiles; tile++) {
+    if (tile > 0) __builtin_amdgcn_s_waitcnt(kWaitAll);
+    QuadTile T;
+    fetch(T);
+    __builtin_amdgcn_s_waitcnt(kWaitLds);  // the slot is read: the next tile may overwrite it
+    if (tile + 1 < ntiles) issue(tile + 1, qtile);
+    compute(tile, T);
+  }
+
+  // ---- the wave's partial: heads 0..G-1 of this kv head
+  l_acc += __shfl_xor(l_acc, 4);
+  l_acc += __shfl_xor(l_acc, 8);
+  l_acc += __shfl_xor(l_acc, 16);
+  l_acc += __shfl_xor(l_acc, 32);
+  wb0 += __shfl_xor(wb0, 4);
+  wb0 += __shfl_xor(wb0, 8);
+  wb0 += __shfl_xor(wb0, 16);
+  wb0 += __shfl_xor(wb0, 32);
+  wb1 += __shfl_xor(wb1, 4);
+  wb1 += __shfl_xor(wb1, 8);
+  wb1 += __shfl_xor(wb1, 16);
+  wb1 += __shfl_xor(wb1, 32);
+  if (q4 == 0) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      if (i < G) {
+        const float b0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wb0), i));
+        const float b1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wb1), i));
+        const size_t part = (size_t(r) * p.H + head0 + i) * p.nchunks + c;
+        float4* po = reinterpret_cast<float4*>(p.po + part * kHD);
+        po[c16] = make_float4(O[0][i] + b0, O[1][i] + b0, O[2][i] + b0, O[3][i] + b0);
+        po[16 + c16] = make_float4(O[4][i] + b1, O[5][i] + b1, O[6][i] + b1, O[7][i] + b1);
+        if (c16 == i) {
+          p.pm[part] = m_run;
+          p.pl[part] = l_acc;
+        }
+      }
+    }
+  }
+}
+
 // ------------------------------------------------------------ 16-bit pass 1
 // K/V of dtype KDT (fp16 or bf16) in (rows, KVH, cap, 128).  Q K^T: lane (key
 // c16, quad q4) supplies dims 32q4 + 4j + i of its key for MFMA j; P V: N-tile ii
@@ -870,20 +1193,27 @@ __global__ __launch_bounds__(256) void decode_combine(CombineParams p) {
 
 using namespace lcl;
 
-// The register-fed pass 1 is the default (it measured faster at every decode config); LOCALS_AMD_DECODE=lds
-// selects the LDS-staged one.
-static int use_lds_pass1() {
+// 8-bit pass 1 variant: the quad kernel for G <= 4, the register-fed one otherwise.  LOCALS_AMD_DECODE=reg
+// or =lds forces the register-fed or the LDS-staged 16x16 kernel (for comparisons).
+enum { kVarAuto = 0, kVarReg = 1, kVarLds = 2 };
+static int decode_variant() {
   static int v = -1;
   if (v < 0) {
     const char* e = getenv("LOCALS_AMD_DECODE");
-    v = (e && e[0] == 'l') ? 1 : 0;
+    v = !e ? kVarAuto : e[0] == 'l' ? kVarLds : e[0] == 'r' ? kVarReg : kVarAuto;
   }
   return v;
 }
 
+static bool use_quad(const DecodeParams& p) { return p.G <= 4 && decode_variant() == kVarAuto; }
+
 template <int QDT, int SDT>
 static void launch_q8_t(dim3 grid, hipStream_t stream, hipEvent_t e0, hipEvent_t e1, const DecodeParams& p) {
-  if (use_lds_pass1()) hipExtLaunchKernelGGL((qkv_pass1_q8_lds<QDT, SDT>), grid, dim3(256), 0, stream, e0, e1, 0, p);
+  if (use_quad(p))
+    hipExtLaunchKernelGGL((qkv_pass1_q8_quad<QDT, SDT>), dim3(grid.x, p.KVH, grid.z), dim3(64), 0, stream, e0, e1, 0,
+                          p);
+  else if (decode_variant() == kVarLds)
+    hipExtLaunchKernelGGL((qkv_pass1_q8_lds<QDT, SDT>), grid, dim3(256), 0, stream, e0, e1, 0, p);
   else hipExtLaunchKernelGGL((qkv_pass1_q8<QDT, SDT>), grid, dim3(256), 0, stream, e0, e1, 0, p);
 }
 
