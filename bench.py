@@ -276,6 +276,8 @@ def main():
     ap.add_argument("--block", type=int, default=None, help="keys a pass-1 workgroup reads (qkv.BLOCK)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--p1-every", type=int, default=1, metavar="K",
+                    help="bracket every K-th step's pass-1 dispatch with HIP events (the roofline sample)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="instead of the bench: K device copies of MIB MiB (the known-size kernel that scales the "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
@@ -347,13 +349,17 @@ def main():
     hip = ev.hip
     hip.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
     hip.hipEventRecord(ev.ev[-2], stream)
+    every = max(1, args.p1_every)
     for i in range(K_):
-        step(i, ev.ev[2 * i], ev.ev[2 * i + 1])
+        if i % every == 0:
+            step(i, ev.ev[2 * i], ev.ev[2 * i + 1])
+        else:
+            step(i)
     hip.hipEventRecord(ev.ev[-1], stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     region_ms = ev.ms(2 * K_, 2 * K_ + 1)
-    p1 = np.array([ev.ms(2 * i, 2 * i + 1) for i in range(K_)])
+    p1 = np.array([ev.ms(2 * i, 2 * i + 1) for i in range(0, K_, every)])
     ev.close()
 
     ms_step = region_ms / K_

@@ -64,6 +64,8 @@ struct DecodeParams {
   float* po;
   int n, cap, H, KVH, G, nslices, nchunks, chunk;
   int kv_rows;  // rows of the KV buffers (B, or n_slots); a slot outside is clamped
+  int R;        // query rows
+  int qwaves, qmint;  // quad pass 1: waves launched, least tiles a wave
   float scale_log2;
   const float* scale_dev;  // if set, the scale is read from device memory (times log2 e in the kernel)
   int qdt, sdt;
@@ -78,6 +80,7 @@ struct CombineParams {
   const int32_t* start;
   const int32_t* nkeys;
   int n, cap, H, nchunks, chunk, odt;
+  int quad, R, KVH, G, qwaves, qmint;  // quad: parts are the stream-K slots of the quad pass 1
 };
 
 __device__ __forceinline__ void row_range(const int32_t* start, const int32_t* nkeys, int n, int cap, int r, int& lo,
@@ -649,7 +652,8 @@ __global__ __launch_bounds__(256) void qkv_pass1_q8_lds(DecodeParams p) {
 // 16 sigma + 4 q4 + 0..3 -- is exactly what lane 16 q4 + 4 sigma + n computed: one DPP
 // row shift by 4 sigma.  P V stays on 16x16x16 MFMA with the V transposition of the
 // register kernel (rows of heads >= 4 are discarded).
-// Loads: a workgroup is one wave owning one key chunk and its partial.  Each 64-key
+// Work: a workgroup is one wave owning an equal share of all tiles (the stream-K split
+// below) and writing one partial per (row, kv head) it touches.  Each 64-key
 // tile (K codes 8 KB, V codes 8 KB, four 256 B scale/bias arrays) arrives by direct
 // buffer->LDS loads of whole 128-byte lines (20 instructions) into the wave's LDS
 // slot; the wave copies the tile into registers, then sends the next tile's loads into
@@ -676,95 +680,168 @@ __device__ __forceinline__ uint32_t row_take(uint32_t x) {
   else return uint32_t(__builtin_amdgcn_update_dpp(0, int(x), 0x100 + SH, 0xf, 0xf, true));
 }
 
+// Stream-K split of the quad pass 1: the (row, kv head, 64-key tile) list in row-major order
+// (a row's tiles are the 64-aligned ones overlapping its keys [lo, hi)) is cut into W equal
+// ranges, W = min(waves launched, total / mint), so every wave gets >= mint tiles and one
+// resident round of waves finishes together whatever the row lengths.  A wave writes one
+// partial for each (row, kv head) stream its range touches, at slot
+// j = wave - (wave holding the stream's first tile); pass 2 recomputes the same split.
+__device__ __forceinline__ int quad_row_tiles(const int32_t* start, const int32_t* nkeys, int n, int cap, int r,
+                                              int& t0, int& lo, int& hi) {
+  row_range(start, nkeys, n, cap, r, lo, hi);
+  if (hi <= lo) {
+    t0 = 0;
+    return 0;
+  }
+  t0 = lo / kQT;
+  return (hi + kQT - 1) / kQT - t0;
+}
+
+// Lane-parallel scans over the rows (64 a step): the tile counts of rows base + lane.
+__device__ __forceinline__ int quad_lane_count(const int32_t* start, const int32_t* nkeys, int n, int cap, int R,
+                                               int row) {
+  int t0, lo, hi;
+  return row < R ? quad_row_tiles(start, nkeys, n, cap, row, t0, lo, hi) : 0;
+}
+
+__device__ __forceinline__ int wave_incl_scan(int x) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_up(x, o);
+    if (lane >= o) x += y;
+  }
+  return x;
+}
+
+// total tiles T (all rows x KVH) and the wave count W of the split; with `row` >= 0 also the tiles of the rows
+// before it (`before`, in row units)
+__device__ __forceinline__ void quad_split(const int32_t* start, const int32_t* nkeys, int n, int cap, int R, int KVH,
+                                           int wlaunch, int mint, long long& T, int& W, int row, long long& before) {
+  const int lane = threadIdx.x & 63;
+  long long t = 0;
+  before = 0;
+  for (int base = 0; base < R; base += 64) {
+    const int c = quad_lane_count(start, nkeys, n, cap, R, base + lane);
+    const int incl = wave_incl_scan(c);
+    if (row >= base && row < base + 64) before = t + __shfl(incl - c, row - base);
+    t += __shfl(incl, 63);
+  }
+  T = t * KVH;
+  W = int(min((long long)wlaunch, max(1LL, T / mint)));
+}
+
+// the row holding global tile g (0 <= g < T) and the global index of its first tile
+__device__ __forceinline__ int quad_locate(const int32_t* start, const int32_t* nkeys, int n, int cap, int R, int KVH,
+                                           long long g, long long& row_first) {
+  const int lane = threadIdx.x & 63;
+  long long acc = 0;
+  for (int base = 0; base < R; base += 64) {
+    const int c = quad_lane_count(start, nkeys, n, cap, R, base + lane);
+    const int incl = wave_incl_scan(c);
+    const long long lo = acc + (long long)(incl - c) * KVH, hi = acc + (long long)incl * KVH;
+    const unsigned long long m = __ballot(c > 0 && g >= lo && g < hi);
+    if (m) {
+      const int l = __ffsll((long long)m) - 1;
+      row_first = acc + (long long)__shfl(incl - c, l) * KVH;
+      return base + l;
+    }
+    acc += (long long)__shfl(incl, 63) * KVH;
+  }
+  row_first = acc;
+  return R;  // not reached for g < T
+}
+
+// the first row after `row` with tiles (R if none)
+__device__ __forceinline__ int quad_next_row(const int32_t* start, const int32_t* nkeys, int n, int cap, int R,
+                                             int row) {
+  const int lane = threadIdx.x & 63;
+  for (int base = row + 1; base < R; base += 64) {
+    const unsigned long long m = __ballot(quad_lane_count(start, nkeys, n, cap, R, base + lane) > 0);
+    if (m) return base + __ffsll((long long)m) - 1;
+  }
+  return R;
+}
+
+// wave holding global tile g: the largest w with w T / W <= g
+__device__ __forceinline__ int quad_wave_of(long long g, long long T, int W) { return int(((g + 1) * W - 1) / T); }
+
+// a (row, kv head) stream of the quad pass 1
+struct QStream {
+  int r, kvh, t0, lo, hi, cnt;
+  long long Gs;  // global index of its first tile
+};
+// its buffer descriptors (built where used, so only one stream's are live at a time)
+struct QRsrc {
+  BufRsrc rk, rv, rks, rkb, rvs, rvb;
+};
+__device__ __forceinline__ QRsrc quad_rsrc(const DecodeParams& p, const QStream& S) {
+  const int slot = p.slots ? min(max(p.slots[S.r], 0), p.kv_rows - 1) : S.r;
+  const size_t tok0 = (size_t(slot) * p.KVH + S.kvh) * p.cap;
+  const uint32_t cap = uint32_t(p.cap);
+  QRsrc d;
+  d.rk = make_rsrc(p.kw + tok0 * 32, cap * 128u);
+  d.rv = make_rsrc(p.vw + tok0 * 32, cap * 128u);
+  d.rks = make_rsrc(static_cast<const uint32_t*>(p.ks) + tok0, cap * 4u);
+  d.rkb = make_rsrc(static_cast<const uint32_t*>(p.kb) + tok0, cap * 4u);
+  d.rvs = make_rsrc(static_cast<const uint32_t*>(p.vs) + tok0, cap * 4u);
+  d.rvb = make_rsrc(static_cast<const uint32_t*>(p.vb) + tok0, cap * 4u);
+  return d;
+}
+// the G query rows of a stream (rows past G read as 0)
+template <int QB>
+__device__ __forceinline__ BufRsrc quad_qrsrc(const DecodeParams& p, const QStream& S) {
+  return make_rsrc(static_cast<const uint8_t*>(p.q) + (size_t(S.r) * p.H + size_t(S.kvh) * p.G) * kHD * QB,
+                   uint32_t(p.G * kHD * QB));
+}
+
 template <int QDT, int SDT>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void qkv_pass1_q8_quad(DecodeParams p) {
-  const int c = blockIdx.x, kvh = blockIdx.y, r = blockIdx.z;
-  int lo, hi;
-  row_range(p.start, p.nkeys, p.n, p.cap, r, lo, hi);
-  const int c0 = c * p.chunk;
-  const int clo = max(lo, c0), chi = min(hi, c0 + p.chunk);
-  if (clo >= chi) return;  // no key of this row in this chunk
-
+  const int wv = blockIdx.x;
   const int lane = threadIdx.x;
-  const int n = lane & 3;             // QK: head column of this lane
+  constexpr int QB = QDT == DT_F32 ? 4 : 2;
+
+  // ---- the split and this wave's first stream (one lane-parallel pass over the rows when R <= 64)
+  long long T, g, gend, row_first;
+  int W, r0;
+  if (p.R <= 64) {
+    const int c = quad_lane_count(p.start, p.nkeys, p.n, p.cap, p.R, lane);
+    const int incl = wave_incl_scan(c);
+    T = (long long)__shfl(incl, 63) * p.KVH;
+    W = int(min((long long)p.qwaves, max(1LL, T / p.qmint)));
+    if (wv >= W) return;
+    g = wv * T / W;
+    gend = (wv + 1) * T / W;
+    if (g >= gend) return;
+    const long long lo_t = (long long)(incl - c) * p.KVH, hi_t = (long long)incl * p.KVH;
+    const unsigned long long m = __ballot(c > 0 && g >= lo_t && g < hi_t);
+    r0 = __ffsll((long long)m) - 1;
+    row_first = (long long)__shfl(incl - c, r0) * p.KVH;
+  } else {
+    long long unused;
+    quad_split(p.start, p.nkeys, p.n, p.cap, p.R, p.KVH, p.qwaves, p.qmint, T, W, -1, unused);
+    if (wv >= W) return;
+    g = wv * T / W;
+    gend = (wv + 1) * T / W;
+    if (g >= gend) return;
+    r0 = quad_locate(p.start, p.nkeys, p.n, p.cap, p.R, p.KVH, g, row_first);
+  }
+
+  const int n = lane & 3;  // QK: head column of this lane
   const int c16 = lane & 15, q4 = lane >> 4;
-  const int G = p.G;                  // <= 4
-  const int head0 = kvh * G;
-  const int slot = p.slots ? min(max(p.slots[r], 0), p.kv_rows - 1) : r;
-  const size_t tok0 = (size_t(slot) * p.KVH + kvh) * p.cap;
-  const uint32_t cap = uint32_t(p.cap);
-  const BufRsrc rk = make_rsrc(p.kw + tok0 * 32, cap * 128u);
-  const BufRsrc rv = make_rsrc(p.vw + tok0 * 32, cap * 128u);
-  const BufRsrc rks = make_rsrc(static_cast<const uint32_t*>(p.ks) + tok0, cap * 4u);
-  const BufRsrc rkb = make_rsrc(static_cast<const uint32_t*>(p.kb) + tok0, cap * 4u);
-  const BufRsrc rvs = make_rsrc(static_cast<const uint32_t*>(p.vs) + tok0, cap * 4u);
-  const BufRsrc rvb = make_rsrc(static_cast<const uint32_t*>(p.vb) + tok0, cap * 4u);
+  const int G = p.G;       // <= 4
 
   __shared__ __attribute__((aligned(16))) uint8_t qtile[kQSlot];
+  __shared__ __attribute__((aligned(16))) uint8_t qraw[4 * kHD * QB];  // the next stream's q as loaded
+  __shared__ __attribute__((aligned(16))) _Float16 qh[4 * kHD];          // this stream's q in fp16
+  constexpr int kWaitAll = (0xF << 8) | (0x7 << 4);        // s_waitcnt vmcnt(0)
+  constexpr int kWaitLds = (0x3 << 14) | (0x7 << 4) | 0xF;  // s_waitcnt lgkmcnt(0)
 
-  const int kb0 = clo & ~(kQT - 1);
-  const int ntiles = (chi - 1 - kb0) / kQT + 1;
   // DMA lane roles: instruction u moves tile keys 8u + (lane >> 3), lane slot (lane & 7)
   const uint32_t dk_lo = 128u * uint32_t(lane >> 3);
   const uint32_t dk_c0 = 16u * uint32_t((lane & 7) ^ ((lane >> 3) & 3));        // hk for u with bit 1 clear
   const uint32_t dk_c1 = 16u * uint32_t((lane & 7) ^ (((lane >> 3) & 3) | 4));  // hk for u with bit 1 set
   const uint32_t dv_c = 16u * uint32_t((lane & 7) ^ (4 * ((lane >> 5) & 1)));
-  auto issue = [&](int tile, uint8_t* S) {
-    const uint32_t kt = uint32_t(kb0 + tile * kQT);
-#pragma unroll
-    for (int u = 0; u < 8; u++) {
-      const uint32_t row = (kt + 8u * u) * 128u + dk_lo;
-      lds_load16(rk, S + 1024 * u, row + ((u & 2) ? dk_c1 : dk_c0));
-      lds_load16(rv, S + 8192 + 1024 * u, row + dv_c);
-    }
-    const uint32_t so = (kt + uint32_t(lane)) * 4u;
-    lds_load4(rks, S + 16384, so);
-    lds_load4(rkb, S + 16384 + 256, so);
-    lds_load4(rvs, S + 16384 + 512, so);
-    lds_load4(rvb, S + 16384 + 768, so);
-  };
-
-  // the G query rows go to LDS by the same route (rows past G read as 0), then become fp16 in place:
-  // qh[128 n + d] = fp16(q[head n][d]), the B operands of the 4x4x4 products
-  constexpr int QB = QDT == DT_F32 ? 4 : 2;
-  __shared__ __attribute__((aligned(16))) uint8_t qraw[4 * kHD * 4];
-  const BufRsrc rq = make_rsrc(static_cast<const uint8_t*>(p.q) + (size_t(r) * p.H + head0) * kHD * QB,
-                               uint32_t(G * kHD * QB));
-  issue(0, qtile);
-#pragma unroll
-  for (int j = 0; j < 2 * QB; j++) lds_load4(rq, qraw + 256 * j, uint32_t(256 * j + 4 * lane));
-  constexpr int kWaitAll = (0xF << 8) | (0x7 << 4);        // s_waitcnt vmcnt(0)
-  constexpr int kWaitLds = (0x3 << 14) | (0x7 << 4) | 0xF;  // s_waitcnt lgkmcnt(0)
-  __builtin_amdgcn_s_waitcnt(kWaitAll);
-  _Float16* qh = reinterpret_cast<_Float16*>(qraw);
-  float qs0 = 0.0f, qs1 = 0.0f;  // sums of head n's fp16 q over dims [0, 64) and [64, 128)
-  {
-    // lane l converts elements 8 l .. 8 l + 7 (head l / 16, group (l / 8) & 1); all reads precede the writes
-    _Float16 t[8];
-    float part = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
-      t[i] = _Float16(ld16<QDT>(qraw, size_t(8 * lane + i)));
-      part += float(t[i]);
-    }
-    __builtin_amdgcn_s_waitcnt(kWaitLds);
-#pragma unroll
-    for (int i = 0; i < 8; i++) qh[8 * lane + i] = t[i];
-    part += __shfl_xor(part, 1);
-    part += __shfl_xor(part, 2);
-    part += __shfl_xor(part, 4);
-    // lane 16 h + 8 g holds the sum of head h, group g
-#pragma unroll
-    for (int h = 0; h < 4; h++) {
-      const float g0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(part), 16 * h));
-      const float g1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(part), 16 * h + 8));
-      qs0 = n == h ? g0 : qs0;
-      qs1 = n == h ? g1 : qs1;
-    }
-  }
-  const float C = p.scale_log2;
-  const float zc0 = 1024.0f * qs0 * C, zc1 = 1024.0f * qs1 * C, qc0 = qs0 * C, qc1 = qs1 * C;
-
   const int tk = quad_key(lane);               // QK row key of this lane
   const uint32_t krow = 128u * uint32_t(tk);
   const int hk = quad_hk(tk);
@@ -772,191 +849,277 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void
   // P V B operands: lane (c16, q4) reads V words of keys 16 sigma + 4 q4 + k, dims 64 g + 4 c16 .. + 3
   const uint32_t vcol = 8192u + 64u * uint32_t(q4 & 1) + 4u * uint32_t(c16);
 
-  float m_run = -INFINITY, l_acc = 0.0f, wb0 = 0.0f, wb1 = 0.0f;
-  f4 O[8];
+  auto issue = [&](const QRsrc& D, const QStream& S, int k) {
+    const uint32_t kt = uint32_t((S.t0 + k) * kQT);
 #pragma unroll
-  for (int ii = 0; ii < 8; ii++) O[ii] = f4{0.0f, 0.0f, 0.0f, 0.0f};
-
-  // the tile as a lane holds it: K chunks of its QK key, the scale words of its 4 score keys, and for each
-  // 16-key sub-tile the V words of keys 16 sigma + 4 q4 + k (dims 64 g + 4 c16 .. + 3) at [sigma][2 k + g]
-  struct QuadTile {
-    u4 k[8];
-    u4 ksc, kbi, vsc, vbi;
-    uint32_t v[4][8];
-  };
-  auto fetch = [&](QuadTile& T) {
-#pragma unroll
-    for (int cc = 0; cc < 8; cc++) T.k[cc] = *reinterpret_cast<const u4*>(qtile + krow + 16 * (cc ^ hk));
-    T.ksc = *reinterpret_cast<const u4*>(qtile + 16384 + 4 * ts0);
-    T.kbi = *reinterpret_cast<const u4*>(qtile + 16640 + 4 * ts0);
-    T.vsc = *reinterpret_cast<const u4*>(qtile + 16896 + 4 * ts0);
-    T.vbi = *reinterpret_cast<const u4*>(qtile + 17152 + 4 * ts0);
-#pragma unroll
-    for (int sg = 0; sg < 4; sg++) {
-#pragma unroll
-      for (int k = 0; k < 4; k++) {
-        const uint32_t row = 128u * uint32_t(16 * sg + 4 * q4 + k);
-        T.v[sg][2 * k + 0] = *reinterpret_cast<const uint32_t*>(qtile + row + vcol);
-        T.v[sg][2 * k + 1] = *reinterpret_cast<const uint32_t*>(qtile + row + (vcol ^ 64u));
-      }
+    for (int u = 0; u < 8; u++) {
+      const uint32_t row = (kt + 8u * u) * 128u + dk_lo;
+      lds_load16(D.rk, qtile + 1024 * u, row + ((u & 2) ? dk_c1 : dk_c0));
+      lds_load16(D.rv, qtile + 8192 + 1024 * u, row + dv_c);
     }
+    const uint32_t so = (kt + uint32_t(lane)) * 4u;
+    lds_load4(D.rks, qtile + 16384, so);
+    lds_load4(D.rkb, qtile + 16384 + 256, so);
+    lds_load4(D.rvs, qtile + 16384 + 512, so);
+    lds_load4(D.rvb, qtile + 16384 + 768, so);
+  };
+  auto issue_q = [&](const QStream& S) {
+    const BufRsrc rq = quad_qrsrc<QB>(p, S);
+#pragma unroll
+    for (int j = 0; j < 2 * QB; j++) lds_load4(rq, qraw + 256 * j, uint32_t(256 * j + 4 * lane));
   };
 
-  auto compute = [&](int tile, const QuadTile& T) {
-    const int kt = kb0 + tile * kQT;
-    // ---- S^T = K Q^T, four chains (group g = chunk >> 2, chunk parity)
-    f4 acc[4];
-#pragma unroll
-    for (int i = 0; i < 4; i++) acc[i] = f4{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-    for (int cc = 0; cc < 8; cc++) {
-      const u4 kv = T.k[cc];
-      const u4 qa = *reinterpret_cast<const u4*>(qh + kHD * n + 16 * cc);
-      const u4 qc = *reinterpret_cast<const u4*>(qh + kHD * n + 16 * cc + 8);
-      f4& a = acc[2 * (cc >> 2) + (cc & 1)];
-      a = mfma4(codes4_to_h4(kv.x), pack_h4(qa.x, qa.y), a);
-      a = mfma4(codes4_to_h4(kv.y), pack_h4(qa.z, qa.w), a);
-      a = mfma4(codes4_to_h4(kv.z), pack_h4(qc.x, qc.y), a);
-      a = mfma4(codes4_to_h4(kv.w), pack_h4(qc.z, qc.w), a);
-    }
-    const uint32_t kscw[4] = {T.ksc.x, T.ksc.y, T.ksc.z, T.ksc.w}, kbiw[4] = {T.kbi.x, T.kbi.y, T.kbi.z, T.kbi.w};
-    const uint32_t vscw[4] = {T.vsc.x, T.vsc.y, T.vsc.z, T.vsc.w}, vbiw[4] = {T.vbi.x, T.vbi.y, T.vbi.z, T.vbi.w};
-    // ---- scores of keys ts0 + m for head n (base-2 logits)
-    const bool full = kt >= clo && kt + kQT <= chi;
-    float s[4];
-    bool valid[4];
-#pragma unroll
-    for (int m = 0; m < 4; m++) {
-      const float a0 = acc[0][m] + acc[1][m], a1 = acc[2][m] + acc[3][m];
-      const float u0 = __builtin_fmaf(a0, C, -zc0), u1 = __builtin_fmaf(a1, C, -zc1);
-      float v = hpart<SDT>(kscw[m], 0) * u0;
-      v = __builtin_fmaf(hpart<SDT>(kscw[m], 1), u1, v);
-      v = __builtin_fmaf(hpart<SDT>(kbiw[m], 0), qc0, v);
-      v = __builtin_fmaf(hpart<SDT>(kbiw[m], 1), qc1, v);
-      const int t = kt + ts0 + m;
-      valid[m] = full || (t >= clo && t < chi);
-      s[m] = valid[m] ? v : -INFINITY;
-    }
-    // ---- tile max of head n over the 16 lanes holding it
-    float tmax = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 4));
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 8));
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
-    const bool need = tmax > m_run + kRescaleThr;
-    if (__any(need)) {
-      const float corr = need ? (m_run == -INFINITY ? 0.0f : fast_exp2(m_run - tmax)) : 1.0f;
-      if (need) m_run = tmax;
-      l_acc *= corr;
-      wb0 *= corr;
-      wb1 *= corr;
-      // P V rows: lane (c16, q4) register i is head 4 q4 + i; heads 0..3 live in lanes 0..15
-#pragma unroll
-      for (int i = 0; i < 4; i++) {
-        const float ci = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(corr), i));
-#pragma unroll
-        for (int ii = 0; ii < 8; ii++) O[ii][i] *= ci;
-      }
-    }
-    float w0[4], w1[4];
-#pragma unroll
-    for (int m = 0; m < 4; m++) {
-      float pr = fast_exp2(s[m] - m_run);
-      float x0 = pr * hpart<SDT>(vscw[m], 0), x1 = pr * hpart<SDT>(vscw[m], 1);
-      float y0 = pr * hpart<SDT>(vbiw[m], 0), y1 = pr * hpart<SDT>(vbiw[m], 1);
-      // garbage scales of keys outside the range must not reach the sums (0 * inf)
-      pr = valid[m] ? pr : 0.0f;
-      x0 = valid[m] ? x0 : 0.0f;
-      x1 = valid[m] ? x1 : 0.0f;
-      y0 = valid[m] ? y0 : 0.0f;
-      y1 = valid[m] ? y1 : 0.0f;
-      l_acc += pr;
-      w0[m] = x0;
-      w1[m] = x1;
-      wb0 += __builtin_fmaf(-1024.0f, x0, y0);
-      wb1 += __builtin_fmaf(-1024.0f, x1, y1);
-    }
-    uint32_t wh[4], wl[4];  // [g][pair]: fp16 hi / lo of w_g for keys m = 0, 1 and 2, 3
-    split_h2(w0[0], w0[1], wh[0], wl[0]);
-    split_h2(w0[2], w0[3], wh[1], wl[1]);
-    split_h2(w1[0], w1[1], wh[2], wl[2]);
-    split_h2(w1[2], w1[3], wh[3], wl[3]);
+  // the stream (row r0, kv head) holding tile g
+  QStream cur;
+  cur.r = r0;
+  cur.cnt = quad_row_tiles(p.start, p.nkeys, p.n, p.cap, r0, cur.t0, cur.lo, cur.hi);
+  cur.kvh = int((g - row_first) / cur.cnt);
+  cur.Gs = row_first + (long long)cur.kvh * cur.cnt;
+  int k0 = int(g - cur.Gs);
+  issue(quad_rsrc(p, cur), cur, k0);
+  issue_q(cur);
 
-    // ---- P V on 16x16x16, one 16-key sub-tile at a time
-    auto pv = [&](auto sig) {
-      constexpr int SG = decltype(sig)::value;
-      const h4 A0h = pack_h4(row_take<4 * SG>(wh[0]), row_take<4 * SG>(wh[1]));
-      const h4 A0l = pack_h4(row_take<4 * SG>(wl[0]), row_take<4 * SG>(wl[1]));
-      const h4 A1h = pack_h4(row_take<4 * SG>(wh[2]), row_take<4 * SG>(wh[3]));
-      const h4 A1l = pack_h4(row_take<4 * SG>(wl[2]), row_take<4 * SG>(wl[3]));
-      const uint32_t (&vd)[8] = T.v[SG];
-      h4 bv[8];
+  for (;;) {
+    // the segment: tiles [k0, k1) of stream cur; its first tile and q are in flight
+    const long long seg_end = min(gend, cur.Gs + cur.cnt);
+    const int k1 = int(seg_end - cur.Gs);
+    const bool more = seg_end < gend;
+    QStream nxt = cur;  // the next stream (the next kv head, or the next row with keys), when there is one
+    if (more) {
+      nxt.Gs = cur.Gs + cur.cnt;
+      if (++nxt.kvh == p.KVH) {
+        nxt.kvh = 0;
+        nxt.r = quad_next_row(p.start, p.nkeys, p.n, p.cap, p.R, cur.r);
+        nxt.cnt = quad_row_tiles(p.start, p.nkeys, p.n, p.cap, nxt.r, nxt.t0, nxt.lo, nxt.hi);
+      }
+    }
+    const QRsrc D = quad_rsrc(p, cur);
+    const int lo = cur.lo, hi = cur.hi;
+    const int head0 = cur.kvh * G;
+
+    __builtin_amdgcn_s_waitcnt(kWaitAll);
+    float qs0 = 0.0f, qs1 = 0.0f;  // sums of head n's fp16 q over dims [0, 64) and [64, 128)
+    {
+      // lane l converts elements 8 l .. 8 l + 7 (head l / 16, group (l / 8) & 1) into qh
+      _Float16 t[8];
+      float part = 0.0f;
 #pragma unroll
-      for (int g = 0; g < 2; g++) {
-        const uint32_t x01 = __builtin_amdgcn_perm(vd[2 + g], vd[g], 0x05010400u);
-        const uint32_t y01 = __builtin_amdgcn_perm(vd[2 + g], vd[g], 0x07030602u);
-        const uint32_t x23 = __builtin_amdgcn_perm(vd[6 + g], vd[4 + g], 0x05010400u);
-        const uint32_t y23 = __builtin_amdgcn_perm(vd[6 + g], vd[4 + g], 0x07030602u);
-        bv[4 * g + 0] = pack_h4(codes_to_h2(x01, 0x00050004u), codes_to_h2(x23, 0x00050004u));
-        bv[4 * g + 1] = pack_h4(codes_to_h2(x01, 0x00070006u), codes_to_h2(x23, 0x00070006u));
-        bv[4 * g + 2] = pack_h4(codes_to_h2(y01, 0x00050004u), codes_to_h2(y23, 0x00050004u));
-        bv[4 * g + 3] = pack_h4(codes_to_h2(y01, 0x00070006u), codes_to_h2(y23, 0x00070006u));
+      for (int i = 0; i < 8; i++) {
+        t[i] = _Float16(ld16<QDT>(qraw, size_t(8 * lane + i)));
+        part += float(t[i]);
       }
 #pragma unroll
-      for (int jj = 0; jj < 4; jj++) {
-        O[jj] = mfma16(A0h, bv[jj], O[jj]);
-        O[4 + jj] = mfma16(A1h, bv[4 + jj], O[4 + jj]);
-      }
+      for (int i = 0; i < 8; i++) qh[8 * lane + i] = t[i];
+      part += __shfl_xor(part, 1);
+      part += __shfl_xor(part, 2);
+      part += __shfl_xor(part, 4);
+      // lane 16 h + 8 g holds the sum of head h, group g
 #pragma unroll
-      for (int jj = 0; jj < 4; jj++) {
-        O[jj] = mfma16(A0l, bv[jj], O[jj]);
-        O[4 + jj] = mfma16(A1l, bv[4 + jj], O[4 + jj]);
+      for (int h = 0; h < 4; h++) {
+        const float g0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(part), 16 * h));
+        const float g1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(part), 16 * h + 8));
+        qs0 = n == h ? g0 : qs0;
+        qs1 = n == h ? g1 : qs1;
+      }
+    }
+    const float C = p.scale_log2;
+    const float zc0 = 1024.0f * qs0 * C, zc1 = 1024.0f * qs1 * C, qc0 = qs0 * C, qc1 = qs1 * C;
+
+    float m_run = -INFINITY, l_acc = 0.0f, wb0 = 0.0f, wb1 = 0.0f;
+    f4 O[8];
+#pragma unroll
+    for (int ii = 0; ii < 8; ii++) O[ii] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    // the tile as a lane holds it: K chunks of its QK key, the scale words of its 4 score keys, and for each
+    // 16-key sub-tile the V words of keys 16 sigma + 4 q4 + k (dims 64 g + 4 c16 .. + 3) at [sigma][2 k + g]
+    struct QuadTile {
+      u4 k[8];
+      u4 ksc, kbi, vsc, vbi;
+      uint32_t v[4][8];
+    };
+    auto fetch = [&](QuadTile& T) {
+  #pragma unroll
+      for (int cc = 0; cc < 8; cc++) T.k[cc] = *reinterpret_cast<const u4*>(qtile + krow + 16 * (cc ^ hk));
+      T.ksc = *reinterpret_cast<const u4*>(qtile + 16384 + 4 * ts0);
+      T.kbi = *reinterpret_cast<const u4*>(qtile + 16640 + 4 * ts0);
+      T.vsc = *reinterpret_cast<const u4*>(qtile + 16896 + 4 * ts0);
+      T.vbi = *reinterpret_cast<const u4*>(qtile + 17152 + 4 * ts0);
+  #pragma unroll
+      for (int sg = 0; sg < 4; sg++) {
+  #pragma unroll
+        for (int k = 0; k < 4; k++) {
+          const uint32_t row = 128u * uint32_t(16 * sg + 4 * q4 + k);
+          T.v[sg][2 * k + 0] = *reinterpret_cast<const uint32_t*>(qtile + row + vcol);
+          T.v[sg][2 * k + 1] = *reinterpret_cast<const uint32_t*>(qtile + row + (vcol ^ 64u));
+        }
       }
     };
-    pv(std::integral_constant<int, 0>{});
-    pv(std::integral_constant<int, 1>{});
-    pv(std::integral_constant<int, 2>{});
-    pv(std::integral_constant<int, 3>{});
-  };
 
-  for (int tile = 0; tile < ntiles; tile++) {
-    if (tile > 0) __builtin_amdgcn_s_waitcnt(kWaitAll);
-    QuadTile T;
-    fetch(T);
-    __builtin_amdgcn_s_waitcnt(kWaitLds);  // the slot is read: the next tile may overwrite it
-    if (tile + 1 < ntiles) issue(tile + 1, qtile);
-    compute(tile, T);
-  }
+    auto compute = [&](int kt, const QuadTile& T) {
+      // ---- S^T = K Q^T, four chains (group g = chunk >> 2, chunk parity)
+      f4 acc[4];
+  #pragma unroll
+      for (int i = 0; i < 4; i++) acc[i] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+  #pragma unroll
+      for (int cc = 0; cc < 8; cc++) {
+        const u4 kv = T.k[cc];
+        const u4 qa = *reinterpret_cast<const u4*>(qh + kHD * n + 16 * cc);
+        const u4 qc = *reinterpret_cast<const u4*>(qh + kHD * n + 16 * cc + 8);
+        f4& a = acc[2 * (cc >> 2) + (cc & 1)];
+        a = mfma4(codes4_to_h4(kv.x), pack_h4(qa.x, qa.y), a);
+        a = mfma4(codes4_to_h4(kv.y), pack_h4(qa.z, qa.w), a);
+        a = mfma4(codes4_to_h4(kv.z), pack_h4(qc.x, qc.y), a);
+        a = mfma4(codes4_to_h4(kv.w), pack_h4(qc.z, qc.w), a);
+      }
+      const uint32_t kscw[4] = {T.ksc.x, T.ksc.y, T.ksc.z, T.ksc.w}, kbiw[4] = {T.kbi.x, T.kbi.y, T.kbi.z, T.kbi.w};
+      const uint32_t vscw[4] = {T.vsc.x, T.vsc.y, T.vsc.z, T.vsc.w}, vbiw[4] = {T.vbi.x, T.vbi.y, T.vbi.z, T.vbi.w};
+      // ---- scores of keys ts0 + m for head n (base-2 logits)
+      const bool full = kt >= lo && kt + kQT <= hi;
+      float s[4];
+      bool valid[4];
+  #pragma unroll
+      for (int m = 0; m < 4; m++) {
+        const float a0 = acc[0][m] + acc[1][m], a1 = acc[2][m] + acc[3][m];
+        const float u0 = __builtin_fmaf(a0, C, -zc0), u1 = __builtin_fmaf(a1, C, -zc1);
+        float v = hpart<SDT>(kscw[m], 0) * u0;
+        v = __builtin_fmaf(hpart<SDT>(kscw[m], 1), u1, v);
+        v = __builtin_fmaf(hpart<SDT>(kbiw[m], 0), qc0, v);
+        v = __builtin_fmaf(hpart<SDT>(kbiw[m], 1), qc1, v);
+        const int t = kt + ts0 + m;
+        valid[m] = full || (t >= lo && t < hi);
+        s[m] = valid[m] ? v : -INFINITY;
+      }
+      // ---- tile max of head n over the 16 lanes holding it
+      float tmax = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
+      tmax = fmaxf(tmax, __shfl_xor(tmax, 4));
+      tmax = fmaxf(tmax, __shfl_xor(tmax, 8));
+      tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
+      tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+      const bool need = tmax > m_run + kRescaleThr;
+      if (__any(need)) {
+        const float corr = need ? (m_run == -INFINITY ? 0.0f : fast_exp2(m_run - tmax)) : 1.0f;
+        if (need) m_run = tmax;
+        l_acc *= corr;
+        wb0 *= corr;
+        wb1 *= corr;
+        // P V rows: lane (c16, q4) register i is head 4 q4 + i; heads 0..3 live in lanes 0..15
+  #pragma unroll
+        for (int i = 0; i < 4; i++) {
+          const float ci = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(corr), i));
+  #pragma unroll
+          for (int ii = 0; ii < 8; ii++) O[ii][i] *= ci;
+        }
+      }
+      float w0[4], w1[4];
+  #pragma unroll
+      for (int m = 0; m < 4; m++) {
+        float pr = fast_exp2(s[m] - m_run);
+        float x0 = pr * hpart<SDT>(vscw[m], 0), x1 = pr * hpart<SDT>(vscw[m], 1);
+        float y0 = pr * hpart<SDT>(vbiw[m], 0), y1 = pr * hpart<SDT>(vbiw[m], 1);
+        // garbage scales of keys outside the range must not reach the sums (0 * inf)
+        pr = valid[m] ? pr : 0.0f;
+        x0 = valid[m] ? x0 : 0.0f;
+        x1 = valid[m] ? x1 : 0.0f;
+        y0 = valid[m] ? y0 : 0.0f;
+        y1 = valid[m] ? y1 : 0.0f;
+        l_acc += pr;
+        w0[m] = x0;
+        w1[m] = x1;
+        wb0 += __builtin_fmaf(-1024.0f, x0, y0);
+        wb1 += __builtin_fmaf(-1024.0f, x1, y1);
+      }
+      uint32_t wh[4], wl[4];  // [g][pair]: fp16 hi / lo of w_g for keys m = 0, 1 and 2, 3
+      split_h2(w0[0], w0[1], wh[0], wl[0]);
+      split_h2(w0[2], w0[3], wh[1], wl[1]);
+      split_h2(w1[0], w1[1], wh[2], wl[2]);
+      split_h2(w1[2], w1[3], wh[3], wl[3]);
 
-  // ---- the wave's partial: heads 0..G-1 of this kv head
-  l_acc += __shfl_xor(l_acc, 4);
-  l_acc += __shfl_xor(l_acc, 8);
-  l_acc += __shfl_xor(l_acc, 16);
-  l_acc += __shfl_xor(l_acc, 32);
-  wb0 += __shfl_xor(wb0, 4);
-  wb0 += __shfl_xor(wb0, 8);
-  wb0 += __shfl_xor(wb0, 16);
-  wb0 += __shfl_xor(wb0, 32);
-  wb1 += __shfl_xor(wb1, 4);
-  wb1 += __shfl_xor(wb1, 8);
-  wb1 += __shfl_xor(wb1, 16);
-  wb1 += __shfl_xor(wb1, 32);
-  if (q4 == 0) {
+      // ---- P V on 16x16x16, one 16-key sub-tile at a time
+      auto pv = [&](auto sig) {
+        constexpr int SG = decltype(sig)::value;
+        const h4 A0h = pack_h4(row_take<4 * SG>(wh[0]), row_take<4 * SG>(wh[1]));
+        const h4 A0l = pack_h4(row_take<4 * SG>(wl[0]), row_take<4 * SG>(wl[1]));
+        const h4 A1h = pack_h4(row_take<4 * SG>(wh[2]), row_take<4 * SG>(wh[3]));
+        const h4 A1l = pack_h4(row_take<4 * SG>(wl[2]), row_take<4 * SG>(wl[3]));
+        const uint32_t (&vd)[8] = T.v[SG];
+        h4 bv[8];
+  #pragma unroll
+        for (int g = 0; g < 2; g++) {
+          const uint32_t x01 = __builtin_amdgcn_perm(vd[2 + g], vd[g], 0x05010400u);
+          const uint32_t y01 = __builtin_amdgcn_perm(vd[2 + g], vd[g], 0x07030602u);
+          const uint32_t x23 = __builtin_amdgcn_perm(vd[6 + g], vd[4 + g], 0x05010400u);
+          const uint32_t y23 = __builtin_amdgcn_perm(vd[6 + g], vd[4 + g], 0x07030602u);
+          bv[4 * g + 0] = pack_h4(codes_to_h2(x01, 0x00050004u), codes_to_h2(x23, 0x00050004u));
+          bv[4 * g + 1] = pack_h4(codes_to_h2(x01, 0x00070006u), codes_to_h2(x23, 0x00070006u));
+          bv[4 * g + 2] = pack_h4(codes_to_h2(y01, 0x00050004u), codes_to_h2(y23, 0x00050004u));
+          bv[4 * g + 3] = pack_h4(codes_to_h2(y01, 0x00070006u), codes_to_h2(y23, 0x00070006u));
+        }
+  #pragma unroll
+        for (int jj = 0; jj < 4; jj++) {
+          O[jj] = mfma16(A0h, bv[jj], O[jj]);
+          O[4 + jj] = mfma16(A1h, bv[4 + jj], O[4 + jj]);
+        }
+  #pragma unroll
+        for (int jj = 0; jj < 4; jj++) {
+          O[jj] = mfma16(A0l, bv[jj], O[jj]);
+          O[4 + jj] = mfma16(A1l, bv[4 + jj], O[4 + jj]);
+        }
+      };
+      pv(std::integral_constant<int, 0>{});
+      pv(std::integral_constant<int, 1>{});
+      pv(std::integral_constant<int, 2>{});
+      pv(std::integral_constant<int, 3>{});
+    };
+
+    for (int k = k0; k < k1; k++) {
+      if (k > k0) __builtin_amdgcn_s_waitcnt(kWaitAll);
+      QuadTile T;
+      fetch(T);
+      __builtin_amdgcn_s_waitcnt(kWaitLds);  // the slot is read: the next tile may overwrite it
+      if (k + 1 < k1) {
+        issue(D, cur, k + 1);
+      } else if (more) {  // the next stream's first tile and q, in flight while this tile computes
+        issue(quad_rsrc(p, nxt), nxt, 0);
+        issue_q(nxt);
+      }
+      compute((cur.t0 + k) * kQT, T);
+    }
+
+    // ---- this segment's partial: heads 0..G-1 of the kv head, slot j of the stream
+    l_acc += __shfl_xor(l_acc, 4);
+    l_acc += __shfl_xor(l_acc, 8);
+    l_acc += __shfl_xor(l_acc, 16);
+    l_acc += __shfl_xor(l_acc, 32);
+    wb0 += __shfl_xor(wb0, 4);
+    wb0 += __shfl_xor(wb0, 8);
+    wb0 += __shfl_xor(wb0, 16);
+    wb0 += __shfl_xor(wb0, 32);
+    wb1 += __shfl_xor(wb1, 4);
+    wb1 += __shfl_xor(wb1, 8);
+    wb1 += __shfl_xor(wb1, 16);
+    wb1 += __shfl_xor(wb1, 32);
+    const int jslot = wv - quad_wave_of(cur.Gs, T, W);
+    if (q4 == 0) {
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-      if (i < G) {
-        const float b0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wb0), i));
-        const float b1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wb1), i));
-        const size_t part = (size_t(r) * p.H + head0 + i) * p.nchunks + c;
-        float4* po = reinterpret_cast<float4*>(p.po + part * kHD);
-        po[c16] = make_float4(O[0][i] + b0, O[1][i] + b0, O[2][i] + b0, O[3][i] + b0);
-        po[16 + c16] = make_float4(O[4][i] + b1, O[5][i] + b1, O[6][i] + b1, O[7][i] + b1);
-        if (c16 == i) {
-          p.pm[part] = m_run;
-          p.pl[part] = l_acc;
+      for (int i = 0; i < 4; i++) {
+        if (i < G) {
+          const float b0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wb0), i));
+          const float b1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wb1), i));
+          const size_t part = (size_t(cur.r) * p.H + head0 + i) * p.nchunks + jslot;
+          float4* po = reinterpret_cast<float4*>(p.po + part * kHD);
+          po[c16] = make_float4(O[0][i] + b0, O[1][i] + b0, O[2][i] + b0, O[3][i] + b0);
+          po[16 + c16] = make_float4(O[4][i] + b1, O[5][i] + b1, O[6][i] + b1, O[7][i] + b1);
+          if (c16 == i) {
+            p.pm[part] = m_run;
+            p.pl[part] = l_acc;
+          }
         }
       }
     }
+
+    if (!more) break;
+    cur = nxt;
+    k0 = 0;
   }
 }
 
@@ -1121,68 +1284,114 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
 }
 
 // ------------------------------------------------------------------- pass 2
-// Grid (row x head, 4 slices of 32 dims).  M = max(sink, max_c m_c) by a block
-// reduction; then 32 chunk lanes x 8 dim lanes (4 dims each) fold w_c = 2^(m_c - M)
-// times o_c and l_c with independent loads in flight, summed in LDS:
-// out = sum_c w_c o_c / (2^(sink - M) + sum_c w_c l_c)  (locals/qkv.py:179-208).
-// No key and no sink: 0.
-constexpr int kCombSlices = 4;
+// Grid (row x head, S slices of 128 / S dims), S = 1..32 chosen so the grid is ~2048
+// workgroups; a workgroup is 8 S part lanes x 32 / S dim lanes (4 dims each).  Part lane c
+// merges parts c, c + 8 S, ... online (running max, rescaled sums).  The
+// first part's loads do not wait for the part count: they go out with the row-length reads
+// and are discarded past the count (the slots exist in the workspace either way).  Lanes are
+// merged by xor shuffles inside each wave, the four waves and the sink in LDS:
+// out = sum_c 2^(m_c - M) o_c / (2^(sink - M) + sum_c 2^(m_c - M) l_c)  (locals/qkv.py:179-208).
+// Parts with m = -inf (no key) weigh 0; no key and no sink: 0.
+constexpr int kCombMaxSlices = 32;
+
+// merge (m2, l2, o2) into (m, l, o)
+__device__ __forceinline__ void lse_merge(float& m, float& l, float4& o, float m2, float l2, const float4& o2) {
+  if (m2 == -INFINITY) return;
+  const float mn = fmaxf(m, m2);
+  const float a = m == -INFINITY ? 0.0f : fast_exp2(m - mn), b = fast_exp2(m2 - mn);
+  o.x = o.x * a + o2.x * b;
+  o.y = o.y * a + o2.y * b;
+  o.z = o.z * a + o2.z * b;
+  o.w = o.w * a + o2.w * b;
+  l = l * a + l2 * b;
+  m = mn;
+}
+
 __global__ __launch_bounds__(256) void decode_combine(CombineParams p) {
   const int rh = blockIdx.x, r = rh / p.H, head = rh % p.H;
-  const int ds = blockIdx.y;
-  const int tid = threadIdx.x;
+  const int ds = blockIdx.y, S = gridDim.y;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int nd = 32 / S, np = 8 * S;        // dim lanes (4 dims each), part lanes
+  const int dl = tid % nd, cs = tid / nd;
+  const size_t base = size_t(rh) * p.nchunks;
+  const float4* po4 = reinterpret_cast<const float4*>(p.po) + ds * nd + dl;
+  // the first part of this lane, loaded before the count is known (slot cs < nchunks always exists)
+  const bool pre = cs < p.nchunks;
+  float m0 = -INFINITY, l0 = 0.0f;
+  float4 o0 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  if (pre) {
+    m0 = p.pm[base + cs];
+    l0 = p.pl[base + cs];
+    o0 = po4[(base + cs) * (kHD / 4)];
+  }
   int lo, hi;
   row_range(p.start, p.nkeys, p.n, p.cap, r, lo, hi);
   int cl = 0, ch = 0;
-  if (hi > lo) {
+  if (p.quad) {
+    long long T, before;
+    int W;
+    quad_split(p.start, p.nkeys, p.n, p.cap, p.R, p.KVH, p.qwaves, p.qmint, T, W, r, before);
+    const long long acc_t = before * p.KVH;
+    int t0, l2, h2;
+    const int cnt = quad_row_tiles(p.start, p.nkeys, p.n, p.cap, r, t0, l2, h2);
+    if (cnt > 0) {
+      const long long Gs = acc_t + (long long)(head / p.G) * cnt;
+      ch = quad_wave_of(Gs + cnt - 1, T, W) - quad_wave_of(Gs, T, W) + 1;
+    }
+  } else if (hi > lo) {
     cl = lo / p.chunk;
     ch = (hi + p.chunk - 1) / p.chunk;
   }
-  const size_t base = size_t(rh) * p.nchunks;
-  const float sink = p.sinks ? p.sinks[head] * kLog2e : -INFINITY;
-  float m = -INFINITY;
-  for (int cc = cl + tid; cc < ch; cc += 256) m = fmaxf(m, p.pm[base + cc]);
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
-  __shared__ float s_red[4];
-  __shared__ float4 s_o[32][8];
-  __shared__ float s_l[32];
-  if ((tid & 63) == 0) s_red[tid >> 6] = m;
-  __syncthreads();
-  const float M = fmaxf(fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3])), sink);
-  const int dl = tid & 7, cs = tid >> 3;
+  float m = -INFINITY, L = 0.0f;
   float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-  float L = 0.0f;
-  if (M != -INFINITY) {
-    const float4* po4 = reinterpret_cast<const float4*>(p.po) + ds * 8 + dl;
-#pragma unroll 4
-    for (int cc = cl + cs; cc < ch; cc += 32) {
-      const float mc = p.pm[base + cc];
-      const float w = mc == -INFINITY ? 0.0f : fast_exp2(mc - M);
-      const float4 o = po4[(base + cc) * (kHD / 4)];
-      acc.x += w * o.x;
-      acc.y += w * o.y;
-      acc.z += w * o.z;
-      acc.w += w * o.w;
-      L += w * p.pl[base + cc];
+  int c = cl + cs;
+  if (cl == 0 && pre) {  // the preloaded part is part cs
+    if (cs < ch) lse_merge(m, L, acc, m0, l0, o0);
+    c += np;
+  }
+#pragma unroll 2
+  for (; c < ch; c += np) lse_merge(m, L, acc, p.pm[base + c], p.pl[base + c], po4[(base + c) * (kHD / 4)]);
+  // part lanes of the wave: lanes differing in the bits above the dim lane
+  for (int x = nd; x < 64; x <<= 1) {
+    const float m2 = __shfl_xor(m, x), l2 = __shfl_xor(L, x);
+    float4 o2;
+    o2.x = __shfl_xor(acc.x, x);
+    o2.y = __shfl_xor(acc.y, x);
+    o2.z = __shfl_xor(acc.z, x);
+    o2.w = __shfl_xor(acc.w, x);
+    lse_merge(m, L, acc, m2, l2, o2);
+  }
+  __shared__ float4 s_o[4][8];
+  __shared__ float s_m[4], s_l[4];
+  if (lane < nd) {
+    s_o[wave][lane] = acc;
+    if (lane == 0) {
+      s_m[wave] = m;
+      s_l[wave] = L;
     }
   }
-  s_o[cs][dl] = acc;
-  if (dl == 0) s_l[cs] = L;
   __syncthreads();
-  if (tid >= 8) return;
+  if (tid >= nd) return;
+  const float sink = p.sinks ? p.sinks[head] * kLog2e : -INFINITY;
+  float M = sink;
   float4 t = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-  float Lt = (sink == -INFINITY || M == -INFINITY) ? 0.0f : fast_exp2(sink - M);
-#pragma unroll 8
-  for (int k = 0; k < 32; k++) {
-    t.x += s_o[k][tid].x;
-    t.y += s_o[k][tid].y;
-    t.z += s_o[k][tid].z;
-    t.w += s_o[k][tid].w;
-    Lt += s_l[k];
+  float Lt = 0.0f;
+#pragma unroll
+  for (int w = 0; w < 4; w++) M = fmaxf(M, s_m[w]);
+  if (M != -INFINITY) {
+    if (sink != -INFINITY) Lt = fast_exp2(sink - M);
+#pragma unroll
+    for (int w = 0; w < 4; w++) {
+      const float f = s_m[w] == -INFINITY ? 0.0f : fast_exp2(s_m[w] - M);
+      t.x += f * s_o[w][tid].x;
+      t.y += f * s_o[w][tid].y;
+      t.z += f * s_o[w][tid].z;
+      t.w += f * s_o[w][tid].w;
+      Lt += f * s_l[w];
+    }
   }
   const float inv = Lt > 0.0f ? 1.0f / Lt : 0.0f;
-  const size_t ob = size_t(rh) * kHD + 32 * ds + 4 * tid;
+  const size_t ob = size_t(rh) * kHD + 4 * nd * ds + 4 * tid;
   store_from_f32(p.out, ob + 0, t.x * inv, p.odt);
   store_from_f32(p.out, ob + 1, t.y * inv, p.odt);
   store_from_f32(p.out, ob + 2, t.z * inv, p.odt);
@@ -1210,8 +1419,7 @@ static bool use_quad(const DecodeParams& p) { return p.G <= 4 && decode_variant(
 template <int QDT, int SDT>
 static void launch_q8_t(dim3 grid, hipStream_t stream, hipEvent_t e0, hipEvent_t e1, const DecodeParams& p) {
   if (use_quad(p))
-    hipExtLaunchKernelGGL((qkv_pass1_q8_quad<QDT, SDT>), dim3(grid.x, p.KVH, grid.z), dim3(64), 0, stream, e0, e1, 0,
-                          p);
+    hipExtLaunchKernelGGL((qkv_pass1_q8_quad<QDT, SDT>), grid, dim3(64), 0, stream, e0, e1, 0, p);
   else if (decode_variant() == kVarLds)
     hipExtLaunchKernelGGL((qkv_pass1_q8_lds<QDT, SDT>), grid, dim3(256), 0, stream, e0, e1, 0, p);
   else hipExtLaunchKernelGGL((qkv_pass1_q8<QDT, SDT>), grid, dim3(256), 0, stream, e0, e1, 0, p);
@@ -1242,6 +1450,13 @@ static void launch_16(int qdt, int kvdt, dim3 grid, hipStream_t stream, const De
   }
 }
 
+// pass 2 dim slices: the largest power of two in [4, 32] keeping the grid within ~2048 workgroups
+static int comb_slices(int rows_heads) {
+  int S = 4;
+  while (S < kCombMaxSlices && (long long)rows_heads * S * 2 <= 2048) S <<= 1;
+  return S;
+}
+
 static int pick_chunk(int block, int extent) {
   if (block > 0) return block;
   (void)extent;
@@ -1252,12 +1467,34 @@ static size_t ws_bytes_for(int R, int H, int nchunks) {
   return size_t(R) * H * nchunks * (2 + kHD) * sizeof(float);
 }
 
+// quad pass 1: least keys a wave = the block (a multiple of 64); slots a (row, head) for `extent` keys
+static int quad_mint(int chunk) { return max(1, chunk / kQT); }
+static int quad_slots(int extent, int chunk) {
+  const int tiles = (max(extent, 1) + kQT - 1) / kQT;
+  return (tiles + quad_mint(chunk) - 1) / quad_mint(chunk) + 1;
+}
+// waves of the quad pass 1: two a SIMD (the kernel's occupancy), one resident round
+static int quad_waves() {
+  static int cache[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+  if (!cache[dev]) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
+    cache[dev] = 2 * 4 * cus;
+    // LOCALS_AMD_DECODE_WAVES overrides the count (a tuning knob: fewer waves than resident slots)
+    const char* e = getenv("LOCALS_AMD_DECODE_WAVES");
+    if (e && atoi(e) > 0) cache[dev] = atoi(e);
+  }
+  return cache[dev];
+}
+
 extern "C" {
 
 size_t lcl_decode_workspace_bytes(int R, int H, int extent, int block) {
   const int chunk = pick_chunk(block, extent);
   const int nchunks = extent > 0 ? (extent + chunk - 1) / chunk : 1;
-  return ws_bytes_for(R, H, nchunks);
+  return ws_bytes_for(R, H, max(nchunks, quad_slots(extent, chunk)));
 }
 
 int lcl_qkv_attend(const void* q, int qdt, const uint32_t* kw, const void* ks, const void* kb, const uint32_t* vw,
@@ -1279,32 +1516,41 @@ int lcl_qkv_attend_ex(const void* q, int qdt, const uint32_t* kw, const void* ks
   if (block < 0 || block % 64) return -1;
   if ((qdt != DT_F16 && qdt != DT_BF16 && qdt != DT_F32) || (sdt != DT_F16 && sdt != DT_BF16)) return -1;
   const int chunk = pick_chunk(block, n);
-  const int nchunks = n > 0 ? (n + chunk - 1) / chunk : 1;
-  if (!workspace || workspace_bytes < ws_bytes_for(B, H, nchunks)) return -3;
   DecodeParams p{};
+  p.G = H / KVH;
+  const bool quad = use_quad(p);
+  // parts a (row, head): the chunks of the grid, or the stream-K slots of the quad pass 1
+  const int nparts = quad ? quad_slots(n, chunk) : (n > 0 ? (n + chunk - 1) / chunk : 1);
+  if (!workspace || workspace_bytes < ws_bytes_for(B, H, nparts)) return -3;
   p.q = q;
   p.kw = kw; p.ks = ks; p.kb = kb;
   p.vw = vw; p.vs = vs; p.vb = vb;
   p.start = start;
   float* ws = static_cast<float*>(workspace);
-  const size_t np = size_t(B) * H * nchunks;
+  const size_t np = size_t(B) * H * nparts;
   p.pm = ws;
   p.pl = ws + np;
   p.po = ws + 2 * np;
-  p.n = n; p.cap = cap; p.H = H; p.KVH = KVH; p.G = H / KVH; p.kv_rows = B;
+  p.n = n; p.cap = cap; p.H = H; p.KVH = KVH; p.kv_rows = B; p.R = B;
   p.nslices = (p.G + 15) / 16;
-  p.nchunks = nchunks; p.chunk = chunk;
+  p.nchunks = nparts; p.chunk = chunk;
   p.scale_log2 = scale * kLog2e;
   p.qdt = qdt; p.sdt = sdt;
+  if (quad) {
+    p.qmint = quad_mint(chunk);
+    const long long tmax = (long long)B * KVH * ((n + kQT - 1) / kQT);
+    p.qwaves = int(min((long long)quad_waves(), max(1LL, tmax / p.qmint)));
+  }
   if (n > 0) {
-    const dim3 grid(nchunks, KVH * p.nslices, B);
+    const dim3 grid = quad ? dim3(p.qwaves) : dim3(nparts, KVH * p.nslices, B);
     hipEvent_t e0 = static_cast<hipEvent_t>(ev_start), e1 = static_cast<hipEvent_t>(ev_stop);
     launch_q8(qdt, sdt, grid, stream, e0, e1, p);
   }
   CombineParams c{};
   c.pm = p.pm; c.pl = p.pl; c.po = p.po; c.sinks = sinks; c.out = out;
-  c.start = start; c.nkeys = nullptr; c.n = n; c.cap = cap; c.H = H; c.nchunks = nchunks; c.chunk = chunk; c.odt = qdt;
-  hipLaunchKernelGGL(decode_combine, dim3(B * H, kCombSlices), dim3(256), 0, stream, c);
+  c.start = start; c.nkeys = nullptr; c.n = n; c.cap = cap; c.H = H; c.nchunks = nparts; c.chunk = chunk; c.odt = qdt;
+  c.quad = quad; c.R = B; c.KVH = KVH; c.G = p.G; c.qwaves = p.qwaves; c.qmint = p.qmint;
+  hipLaunchKernelGGL(decode_combine, dim3(B * H, comb_slices(B * H)), dim3(256), 0, stream, c);
   return int(hipGetLastError());
 }
 
@@ -1340,7 +1586,7 @@ int lcl_ragged_attention(const void* q, int qdt, const void* keys, const void* v
   c.pm = p.pm; c.pl = p.pl; c.po = p.po; c.sinks = nullptr; c.out = out;
   c.start = nullptr; c.nkeys = nkeys; c.n = cap; c.cap = cap; c.H = H; c.nchunks = nchunks; c.chunk = chunk;
   c.odt = qdt;
-  hipLaunchKernelGGL(decode_combine, dim3(R * H, kCombSlices), dim3(256), 0, stream, c);
+  hipLaunchKernelGGL(decode_combine, dim3(R * H, comb_slices(R * H)), dim3(256), 0, stream, c);
   return int(hipGetLastError());
 }
 
