@@ -363,6 +363,8 @@ def main():
     ev.close()
 
     ms_step = region_ms / K_
+    # the pass-1 kernel the library runs for this head ratio (4x4x4-MFMA stream-K kernel for G <= 4)
+    kernel = "qkv_pass1_q8_quad" if H // KVH <= 4 else "qkv_pass1_q8"
     b_step, b_p1 = step_bytes(cfg)
     value = b_step / (ms_step * 1e-3) / 1e9
     p1_us = float(p1.mean() * 1e3)
@@ -387,11 +389,11 @@ def main():
                    "bytes_per_step": b_step, "buffer_sets": len(sets), "kv": "MLX affine 8-bit, group 64",
                    "compute": "u8 codes -> fp16 MFMA (exact), fp32 accumulate", "block": qkv.BLOCK or "auto",
                    "wall_s_timed": round(wall, 4)},
-        "roofline": {"bound": "hbm", "kernel": "qkv_pass1_q8", "achieved": round(achieved, 1),
+        "roofline": {"bound": "hbm", "kernel": kernel, "achieved": round(achieved, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "avg_us": round(p1_us, 2), "p10_us": round(float(np.percentile(p1, 10)) * 1e3, 2),
                      "p90_us": round(float(np.percentile(p1, 90)) * 1e3, 2), "bytes_per_launch": b_p1,
-                     "traffic": _traffic(cfg["name"])},
+                     "traffic": _traffic(cfg["name"], kernel)},
         "cpu_baseline": None,
     }
     if cfg["name"] == "c4":
@@ -407,14 +409,15 @@ def main():
     print(json.dumps(line), flush=True)
 
 
-def _traffic(name):
-    """HBM bytes a pass-1 launch moved, from the committed rocprofv3 --pmc summary, or None."""
+def _traffic(name, kernel):
+    """HBM bytes a pass-1 launch moved, from the committed rocprofv3 --pmc summary of this kernel, or None."""
     path = os.path.join(ROOT, "profiles", f"decode_q8_{name}_traffic.json")
     try:
         with open(path) as f:
-            return json.load(f).get("traffic_bytes_per_launch")
+            d = json.load(f)
     except (OSError, ValueError):
         return None
+    return d.get("traffic_bytes_per_launch") if d.get("kernel") == kernel else None
 
 
 if __name__ == "__main__":
