@@ -276,7 +276,7 @@ def main():
     ap.add_argument("--block", type=int, default=None, help="keys a pass-1 workgroup reads (qkv.BLOCK)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--p1-every", type=int, default=1, metavar="K",
+    ap.add_argument("--p1-every", type=int, default=4, metavar="K",
                     help="bracket every K-th step's pass-1 dispatch with HIP events (the roofline sample)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="instead of the bench: K device copies of MIB MiB (the known-size kernel that scales the "
