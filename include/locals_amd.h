@@ -86,7 +86,9 @@ int lcl_quantize_append(const void* k, const void* v, int dt, uint32_t* kw, void
 int lcl_dequantize(const uint32_t* words, const void* scales, const void* biases, int sdt, long long rows, int D,
                    void* out, int odt, void* stream);
 
-/* Bytes of split-K workspace for lcl_sdpa (B rows, H heads, L queries, N keys). */
+/* Bytes of split-K workspace for lcl_sdpa (B rows, H heads, L queries, N keys, key chunk
+ * `block`, 0 = the library's choice).  0 when the call needs none: with a single chunk,
+ * pass 1 writes the output itself and the workspace pointer may be NULL. */
 size_t lcl_sdpa_workspace_bytes(int B, int H, int L, int N, int block);
 
 /* MLX scaled_dot_product_attention(q, k, v, scale, mask, sinks) as the reference

@@ -41,6 +41,9 @@ constexpr int kKT = 64;                 // keys a tile
 constexpr int kKsStride = 136;          // halves a K row in LDS (272 B: 16 B aligned, 4-bank skew a row)
 constexpr int kVtStride = 72;           // halves a V^T row in LDS (144 B: 36-bank skew a row)
 constexpr float kThr = 6.0f;
+// V^T row d keeps its 16 four-key slots XOR-permuted by (d >> 3) & 15: the staging writes, which take 8
+// consecutive rows a thread and rows 8 apart across a wave's lanes, then fall in distinct banks
+__device__ __forceinline__ int vt_swz(int d) { return (d >> 3) & 15; }
 
 enum MaskKind { MK_NONE = 0, MK_CAUSAL = 1, MK_TREE = 2, MK_DENSE = 3 };
 enum KvFmt { KV_Q8 = 0, KV_16 = 1 };
@@ -66,6 +69,8 @@ struct SdpaParams {
   float* po;
   float scale_log2;
   int B, H, KVH, G, L, N, cap, nchunks, chunk, nrowblocks, mask;
+  void* out;  // direct: one chunk covers every key, so pass 1 writes the normalized output (B, H, L, 128), dtype odt
+  int direct, odt;
 };
 
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
@@ -140,15 +145,20 @@ __global__ __launch_bounds__(256) void sdpa_pass1(SdpaParams p) {
   const int klo = max(slo, c * p.chunk);
   int khi = min(p.N, (c + 1) * p.chunk);
   if constexpr (MASK == MK_CAUSAL) khi = min(khi, p.N - p.L + last_q + 1);
-  if (klo >= khi) {  // uniform: nothing here; rows record an empty part
-    if (q4 == 0) {
+  if (klo >= khi) {  // uniform: nothing here; rows record an empty part (or, direct, a zero output)
 #pragma unroll
-      for (int r = 0; r < RT; r++)
-        if (real[r]) {
-          const size_t part = ((size_t(b) * p.H + head[r]) * p.L + qi[r]) * p.nchunks + c;
-          p.pm[part] = -INFINITY;
-          p.pl[part] = 0.0f;
-        }
+    for (int r = 0; r < RT; r++) {
+      if (!real[r]) continue;
+      const size_t row = (size_t(b) * p.H + head[r]) * p.L + qi[r];
+      if (p.direct) {
+#pragma unroll
+        for (int dd = 0; dd < 8; dd++)
+#pragma unroll
+          for (int i = 0; i < 4; i++) store_from_f32(p.out, row * kD + 16 * dd + 4 * q4 + i, 0.0f, p.odt);
+      } else if (q4 == 0) {
+        p.pm[row * p.nchunks + c] = -INFINITY;
+        p.pl[row * p.nchunks + c] = 0.0f;
+      }
     }
     return;
   }
@@ -322,7 +332,7 @@ __global__ __launch_bounds__(256) void sdpa_pass1(SdpaParams p) {
       const uint32_t m23 = (vin[2] ? 0xffffu : 0u) | (vin[3] ? 0xffff0000u : 0u);
 #pragma unroll
       for (int e = 0; e < 8; e++)
-        *reinterpret_cast<uint2*>(&Vt[buf][(8 * vdq + e) * kVtStride + 4 * vkq]) =
+        *reinterpret_cast<uint2*>(&Vt[buf][(8 * vdq + e) * kVtStride + 4 * (vkq ^ vt_swz(8 * vdq + e))]) =
             make_uint2(pr[e][0] & m01, pr[e][1] & m23);
     }
   };
@@ -405,8 +415,10 @@ __global__ __launch_bounds__(256) void sdpa_pass1(SdpaParams p) {
         const uint4 pb = make_uint4(pw[2 * u][0], pw[2 * u][1], pw[2 * u + 1][0], pw[2 * u + 1][1]);
 #pragma unroll
         for (int dd = 0; dd < 8; dd++) {
-          const uint16_t* vrow = &Vt[buf][(16 * dd + c16) * kVtStride + 32 * u + 4 * q4];
-          const uint2 lo = *reinterpret_cast<const uint2*>(vrow), hi = *reinterpret_cast<const uint2*>(vrow + 16);
+          const int vr = 16 * dd + c16, sw = vt_swz(vr);
+          const uint16_t* vrow = &Vt[buf][vr * kVtStride];
+          const uint2 lo = *reinterpret_cast<const uint2*>(vrow + 4 * ((8 * u + q4) ^ sw));
+          const uint2 hi = *reinterpret_cast<const uint2*>(vrow + 4 * ((8 * u + 4 + q4) ^ sw));
           O[r][dd] = mma32<MT>(make_uint4(lo.x, lo.y, hi.x, hi.y), pb, O[r][dd]);
         }
       }
@@ -435,6 +447,22 @@ __global__ __launch_bounds__(256) void sdpa_pass1(SdpaParams p) {
     l += __shfl_xor(l, 16);
     l += __shfl_xor(l, 32);
     if (!real[r]) continue;
+    if (p.direct) {  // the only chunk: join with the sink here, as sdpa_combine would
+      const size_t row = (size_t(b) * p.H + head[r]) * p.L + qi[r];
+      const float sink = p.sinks ? p.sinks[head[r]] * kLog2e : -INFINITY;
+      const float M = fmaxf(m_run[r], sink);
+      float f = 0.0f, Lt = 0.0f;
+      if (M != -INFINITY) {
+        f = m_run[r] == -INFINITY ? 0.0f : fast_exp2(m_run[r] - M);
+        Lt = f * l + (sink == -INFINITY ? 0.0f : fast_exp2(sink - M));
+      }
+      const float w = Lt > 0.0f ? f / Lt : 0.0f;
+#pragma unroll
+      for (int dd = 0; dd < 8; dd++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) store_from_f32(p.out, row * kD + 16 * dd + 4 * q4 + i, O[r][dd][i] * w, p.odt);
+      continue;
+    }
     const size_t part = ((size_t(b) * p.H + head[r]) * p.L + qi[r]) * p.nchunks + c;
     if (q4 == 0) {
       p.pm[part] = m_run[r];
@@ -487,7 +515,8 @@ __global__ __launch_bounds__(256) void sdpa_combine(SdpaCombineParams p) {
 template <int QDT, int SDT, int FMT, int MT, int MASK>
 static void launch_rt(int rt, dim3 grid, hipStream_t s, hipEvent_t e0, hipEvent_t e1, const SdpaParams& p) {
   (void)rt;
-  hipExtLaunchKernelGGL((sdpa_pass1<QDT, SDT, FMT, MT, MASK, 1>), grid, dim3(256), 0, s, e0, e1, 0, p);
+  if (rt == 2) hipExtLaunchKernelGGL((sdpa_pass1<QDT, SDT, FMT, MT, MASK, 2>), grid, dim3(256), 0, s, e0, e1, 0, p);
+  else hipExtLaunchKernelGGL((sdpa_pass1<QDT, SDT, FMT, MT, MASK, 1>), grid, dim3(256), 0, s, e0, e1, 0, p);
 }
 
 template <int QDT, int SDT, int FMT, int MT>
@@ -519,14 +548,23 @@ static void launch_fmt(int qdt, int sdt, int rt, dim3 grid, hipStream_t s, hipEv
 
 using namespace lcl;
 
-static int sdpa_chunk(int block) { return block > 0 ? block : 512; }
+// Keys a pass-1 workgroup reads: the caller's block, or enough chunks that the grid (about B H L / 64 row blocks
+// times the chunks) fills one resident round of ~512 workgroups -- no more: every extra chunk adds a 520-byte part
+// per row to write and read back.  One chunk (most prefill) writes the output directly.
+static int sdpa_chunk(int block, int B, int H, int L, int N) {
+  if (block > 0) return block;
+  const int tiles = max(1, (N + kKT - 1) / kKT);
+  const long long rowblocks = max(1LL, ((long long)B * H * L + 63) / 64);
+  const int want = int(min((long long)tiles, max(1LL, (512 + rowblocks - 1) / rowblocks)));
+  return ((tiles + want - 1) / want) * kKT;
+}
 
 extern "C" {
 
 size_t lcl_sdpa_workspace_bytes(int B, int H, int L, int N, int block) {
-  const int chunk = sdpa_chunk(block);
+  const int chunk = sdpa_chunk(block, B, H, L, N);
   const int nchunks = N > 0 ? (N + chunk - 1) / chunk : 1;
-  return size_t(B) * H * L * nchunks * (2 + kD) * sizeof(float);
+  return nchunks > 1 ? size_t(B) * H * L * nchunks * (2 + kD) * sizeof(float) : 0;
 }
 
 int lcl_sdpa_ex(const void* q, int qdt, int kvfmt, const uint32_t* kw, const void* ks, const void* kb,
@@ -553,9 +591,10 @@ int lcl_sdpa_ex(const void* q, int qdt, int kvfmt, const uint32_t* kw, const voi
   if (mask_kind == MK_CAUSAL && L > N) return -1;
   if (mask_kind == MK_TREE && (!tree || L > 64 || L > N)) return -2;
   if (mask_kind == MK_DENSE && !dense) return -1;
-  const int chunk = sdpa_chunk(block);
+  const int chunk = sdpa_chunk(block, B, H, L, N);
   const int nchunks = N > 0 ? (N + chunk - 1) / chunk : 1;
-  if (!workspace || workspace_bytes < lcl_sdpa_workspace_bytes(B, H, L, N, block)) return -3;
+  const size_t need = lcl_sdpa_workspace_bytes(B, H, L, N, block);
+  if (need && (!workspace || workspace_bytes < need)) return -3;
   SdpaParams p{};
   p.q = q;
   p.kw = kw; p.ks = ks; p.kb = kb; p.vw = vw; p.vs = vs; p.vb = vb; p.kf = kf; p.vf = vf;
@@ -569,6 +608,7 @@ int lcl_sdpa_ex(const void* q, int qdt, int kvfmt, const uint32_t* kw, const voi
   p.scale_log2 = scale * kLog2e;
   p.B = B; p.H = H; p.KVH = KVH; p.G = H / KVH; p.L = L; p.N = N; p.cap = cap;
   p.nchunks = nchunks; p.chunk = chunk; p.mask = mask_kind;
+  p.direct = nchunks == 1; p.out = out; p.odt = qdt;
   // one row tile a wave (64 rows a workgroup): two (128 rows) would reuse each staged tile twice as often but
   // need ~370 registers a lane (one wave a SIMD), which measured slower
   const int rows = L * p.G;
@@ -580,8 +620,10 @@ int lcl_sdpa_ex(const void* q, int qdt, int kvfmt, const uint32_t* kw, const voi
     if (kvfmt == KV_Q8) launch_fmt<KV_Q8>(qdt, kvdt, rt, grid, stream, e0, e1, p);
     else launch_fmt<KV_16>(qdt, kvdt, rt, grid, stream, e0, e1, p);
   }
-  SdpaCombineParams c{p.pm, p.pl, p.po, sinks, out, B * H * L, H, L, nchunks, qdt};
-  hipLaunchKernelGGL(sdpa_combine, dim3((B * H * L + 3) / 4), dim3(256), 0, stream, c);
+  if (!p.direct) {
+    SdpaCombineParams c{p.pm, p.pl, p.po, sinks, out, B * H * L, H, L, nchunks, qdt};
+    hipLaunchKernelGGL(sdpa_combine, dim3((B * H * L + 3) / 4), dim3(256), 0, stream, c);
+  }
   return int(hipGetLastError());
 }
 

@@ -19,6 +19,18 @@ from tests.inputs import normal16, q8_cache, rng, to_torch, triple_to_torch
 pytestmark = pytest.mark.gpu
 
 
+@pytest.fixture(autouse=True, params=[0, 64, 1 << 20], ids=["auto-chunks", "chunk64", "one-chunk"])
+def sdpa_block(request):
+    """Every case runs with the library's chunking, with 64-key chunks (many parts, pass 2 joins them) and with a
+    single chunk (pass 1 writes the output itself)."""
+    from locals_amd import sdpa
+
+    old = sdpa.BLOCK
+    sdpa.BLOCK = request.param
+    yield request.param
+    sdpa.BLOCK = old
+
+
 def _np(t):
     return t.float().cpu().numpy().astype(np.float64)
 
