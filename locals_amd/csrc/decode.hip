@@ -388,12 +388,6 @@ constexpr int kBlk = 64;                        // keys a block
 constexpr int kBlkBytes = 8192 + 8192 + 4 * 256; // K codes, V codes, ks/kb/vs/vb
 constexpr int kRing = 3;  // blocks in the ring
 
-__device__ __forceinline__ void lds_load16(BufRsrc r, void* lds, uint32_t voff) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)(lds), 16, voff, 0, 0, kNT);
-}
-__device__ __forceinline__ void lds_load4(BufRsrc r, void* lds, uint32_t voff) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)(lds), 4, voff, 0, 0, kNT);
-}
 
 template <int QDT, int SDT>
 __global__ __launch_bounds__(256) void qkv_pass1_q8_lds(DecodeParams p) {

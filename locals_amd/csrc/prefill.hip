@@ -40,6 +40,7 @@ constexpr int kD = 128;
 constexpr int kKT = 64;                 // keys a tile
 constexpr int kKsStride = 136;          // halves a K row in LDS (272 B: 16 B aligned, 4-bank skew a row)
 constexpr int kVtStride = 72;           // halves a V^T row in LDS (144 B: 36-bank skew a row)
+constexpr int kRawSlot = 8192 + 8192 + 1024;  // an 8-bit raw tile: K codes, V codes, ks / kb / vs / vb
 constexpr float kThr = 6.0f;
 // V^T row d keeps its 16 four-key slots XOR-permuted by (d >> 3) & 15: the staging writes, which take 8
 // consecutive rows a thread and rows 8 apart across a wave's lanes, then fall in distinct banks
@@ -123,10 +124,10 @@ struct RawTile {
 // chunk c.  Per 64-key tile: the next tile's raw bytes are loaded into registers while this tile's MFMAs run,
 // then dequantized into the other LDS buffer (double-buffered, one barrier a tile).
 template <int QDT, int SDT, int FMT, int MT, int MASK, int RT>
-__global__ __launch_bounds__(256) void sdpa_pass1(SdpaParams p) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void sdpa_pass1(SdpaParams p) {
   const int c = blockIdx.x, rb = blockIdx.y;
   const int b = blockIdx.z / p.KVH, kvh = blockIdx.z % p.KVH;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63, tid = threadIdx.x;
   const int c16 = lane & 15, q4 = lane >> 4;
   const int R = p.L * p.G;
   const int row0 = 64 * RT * rb;
@@ -142,9 +143,10 @@ __global__ __launch_bounds__(256) void sdpa_pass1(SdpaParams p) {
   }
   const int last_q = min(R - 1, row0 + 64 * RT - 1) / p.G;
   const int slo = p.start ? max(p.start[b], 0) : 0;
-  const int klo = max(slo, c * p.chunk);
+  const int klo = __builtin_amdgcn_readfirstlane(max(slo, c * p.chunk));
   int khi = min(p.N, (c + 1) * p.chunk);
   if constexpr (MASK == MK_CAUSAL) khi = min(khi, p.N - p.L + last_q + 1);
+  khi = __builtin_amdgcn_readfirstlane(khi);
   if (klo >= khi) {  // uniform: nothing here; rows record an empty part (or, direct, a zero output)
 #pragma unroll
     for (int r = 0; r < RT; r++) {
@@ -163,8 +165,13 @@ __global__ __launch_bounds__(256) void sdpa_pass1(SdpaParams p) {
     return;
   }
 
-  __shared__ __attribute__((aligned(16))) uint16_t Ks[2][kKT * kKsStride];
-  __shared__ __attribute__((aligned(16))) uint16_t Vt[2][kD * kVtStride];
+  // 8-bit: raw tiles arrive by direct buffer->LDS loads into two named slots (one in flight while the other is
+  // staged) and are dequantized into a single operand buffer; 16-bit: register prefetch, two operand buffers
+  constexpr int NB = FMT == KV_Q8 ? 1 : 2;
+  __shared__ __attribute__((aligned(16))) uint16_t Ks[NB][kKT * kKsStride];
+  __shared__ __attribute__((aligned(16))) uint16_t Vt[NB][kD * kVtStride];
+  __shared__ __attribute__((aligned(16))) uint8_t raw0[FMT == KV_Q8 ? kRawSlot : 16];
+  __shared__ __attribute__((aligned(16))) uint8_t raw1[FMT == KV_Q8 ? kRawSlot : 16];
 
   // Q^T as B operands: qb[r][kk] = q[row][32 kk + 8 q4 + j]
   uint4 qb[RT][4];
@@ -199,10 +206,13 @@ __global__ __launch_bounds__(256) void sdpa_pass1(SdpaParams p) {
     rk = make_rsrc(static_cast<const uint16_t*>(p.kf) + tok0 * kD, cap * 256u);
     rv = make_rsrc(static_cast<const uint16_t*>(p.vf) + tok0 * kD, cap * 256u);
   }
+  // 8-bit DMA: the scale / bias array this wave sends (wave 0 K scales, 1 K biases, 2 V scales, 3 V biases)
+  const void* sarr = FMT != KV_Q8 ? p.kf : wave == 0 ? p.ks : wave == 1 ? p.kb : wave == 2 ? p.vs : p.vb;
+  const BufRsrc rsw = make_rsrc(static_cast<const uint16_t*>(sarr) + tok0 * 2, cap * 4u);
   const int kkey = tid >> 2, kpart = tid & 3;   // K staging: one key, 32 dims
   const int vkq = tid >> 4, vdq = tid & 15;     // V staging: keys 4 vkq .. +3, dims 8 vdq .. +7
 
-  auto load = [&](int t0, RawTile& T) {
+  auto load = [&](int t0, RawTile& T) __attribute__((always_inline)) {
     const uint32_t kk = uint32_t(t0 + kkey);
     if constexpr (FMT == KV_Q8) {
       T.k[0] = buf_load_b128(rk, kk * 128u + 32u * kpart, 0);
@@ -225,8 +235,35 @@ __global__ __launch_bounds__(256) void sdpa_pass1(SdpaParams p) {
     }
   };
 
+  // 8-bit raw tile in LDS: K codes (key-major 128 B rows, 8 KB), V codes (8 KB), ks / kb / vs / vb words (256 B
+  // each).  Wave w sends K and V rows 16 w .. 16 w + 15 (two 1 KB pieces each) and the w-th scale array.
+  auto dma = [&](int t0, uint8_t* S) __attribute__((always_inline)) {
+    const uint32_t base = uint32_t(t0) * 128u + uint32_t(wave) * 2048u + 16u * uint32_t(lane);
+    lds_load16(rk, S + 2048 * wave, base);
+    lds_load16(rk, S + 2048 * wave + 1024, base + 1024u);
+    lds_load16(rv, S + 8192 + 2048 * wave, base);
+    lds_load16(rv, S + 8192 + 2048 * wave + 1024, base + 1024u);
+    lds_load4(rsw, S + 16384 + 256 * wave, (uint32_t(t0) + uint32_t(lane)) * 4u);
+  };
+  // the thread's share of a raw tile in LDS, as the register-prefetch path would hold it
+  auto load_lds = [&](const uint8_t* S, RawTile& T) __attribute__((always_inline)) {
+    const uint8_t* kr = S + kkey * 128 + 32 * kpart;
+    T.k[0] = *reinterpret_cast<const u4*>(kr);
+    T.k[1] = *reinterpret_cast<const u4*>(kr + 16);
+    T.ks = *reinterpret_cast<const uint32_t*>(S + 16384 + 4 * kkey);
+    T.kb = *reinterpret_cast<const uint32_t*>(S + 16640 + 4 * kkey);
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      const int vk = 4 * vkq + k;
+      const uint2 w = *reinterpret_cast<const uint2*>(S + 8192 + vk * 128 + 8 * vdq);
+      T.v[k] = u4{w.x, w.y, 0u, 0u};
+      T.vs[k] = *reinterpret_cast<const uint32_t*>(S + 16896 + 4 * vk);
+      T.vb[k] = *reinterpret_cast<const uint32_t*>(S + 17152 + 4 * vk);
+    }
+  };
+
   // dequantize (8-bit) or copy (16-bit) a staged tile into LDS buffer `buf`; keys outside [klo, khi) become 0
-  auto stage = [&](int t0, const RawTile& T, int buf) {
+  auto stage = [&](int t0, const RawTile& T, int buf) __attribute__((always_inline)) {
     {
       const int kg = t0 + kkey;
       const bool kin = kg >= klo && kg < khi;
@@ -357,19 +394,26 @@ __global__ __launch_bounds__(256) void sdpa_pass1(SdpaParams p) {
     if constexpr (MASK == MK_DENSE) drow[r] = p.dense + b * p.msb + head[r] * p.msh + qi[r] * p.msq;
   }
 
-  auto compute = [&](int t0, int buf) {
+  // Each K / V^T operand fragment is read from LDS once and applied to every row tile of the wave, so a
+  // fragment is live for RT MFMAs only (the row tiles' scores, P and O are what stays in registers).
+  auto compute = [&](int t0, int buf) __attribute__((always_inline)) {
+    // S^T = K Q^T: st[r][t][i] = S[row][t0 + 16 t + 4 q4 + i]
+    f4 st[RT][4];
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+#pragma unroll
+      for (int r = 0; r < RT; r++) st[r][t] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+      const uint16_t* krow = &Ks[buf][(16 * t + c16) * kKsStride + 8 * q4];
+#pragma unroll
+      for (int kk = 0; kk < 4; kk++) {
+        const uint4 kf = *reinterpret_cast<const uint4*>(krow + 32 * kk);
+#pragma unroll
+        for (int r = 0; r < RT; r++) st[r][t] = mma32<MT>(kf, qb[r][kk], st[r][t]);
+      }
+    }
+    uint4 pb[RT][2];  // P^T as B operands: k index 8 q4 + j <-> key 32 u + (j < 4 ? 4 q4 + j : 16 + 4 q4 + j - 4)
 #pragma unroll
     for (int r = 0; r < RT; r++) {
-      // S^T = K Q^T: st[t][i] = S[row][t0 + 16 t + 4 q4 + i]
-      f4 st[4];
-#pragma unroll
-      for (int t = 0; t < 4; t++) {
-        f4 a = f4{0.0f, 0.0f, 0.0f, 0.0f};
-        const uint16_t* krow = &Ks[buf][(16 * t + c16) * kKsStride + 8 * q4];
-#pragma unroll
-        for (int kk = 0; kk < 4; kk++) a = mma32<MT>(*reinterpret_cast<const uint4*>(krow + 32 * kk), qb[r][kk], a);
-        st[t] = a;
-      }
       float tmax = -INFINITY;
 #pragma unroll
       for (int t = 0; t < 4; t++) {
@@ -383,9 +427,9 @@ __global__ __launch_bounds__(256) void sdpa_pass1(SdpaParams p) {
             ok = ok & ((d < 0) | (((tbits[r] >> (d & 63)) & 1ull) != 0ull));
           }
           if constexpr (MASK == MK_DENSE) ok = ok & (drow[r][min(max(j, 0), p.N - 1) * p.msk] != 0);
-          const float s = ok ? st[t][i] * p.scale_log2 : -INFINITY;
-          st[t][i] = s;
-          tmax = fmaxf(tmax, s);
+          const float sc = ok ? st[r][t][i] * p.scale_log2 : -INFINITY;
+          st[r][t][i] = sc;
+          tmax = fmaxf(tmax, sc);
         }
       }
       tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
@@ -403,41 +447,78 @@ __global__ __launch_bounds__(256) void sdpa_pass1(SdpaParams p) {
         float pv[4];
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-          pv[i] = fast_exp2(st[t][i] - m_run[r]);  // -inf -> 0
+          pv[i] = fast_exp2(st[r][t][i] - m_run[r]);  // -inf -> 0
           l_acc[r] += pv[i];
         }
         pw[t][0] = pack2<MT>(pv[0], pv[1]);
         pw[t][1] = pack2<MT>(pv[2], pv[3]);
       }
-      // O^T += V^T P^T, 32 keys a step: k index 8 q4 + j <-> key 32 u + (j < 4 ? 4 q4 + j : 16 + 4 q4 + j - 4)
+      pb[r][0] = make_uint4(pw[0][0], pw[0][1], pw[1][0], pw[1][1]);
+      pb[r][1] = make_uint4(pw[2][0], pw[2][1], pw[3][0], pw[3][1]);
+    }
+    // O^T += V^T P^T, 32 keys a step
 #pragma unroll
-      for (int u = 0; u < 2; u++) {
-        const uint4 pb = make_uint4(pw[2 * u][0], pw[2 * u][1], pw[2 * u + 1][0], pw[2 * u + 1][1]);
+    for (int u = 0; u < 2; u++) {
 #pragma unroll
-        for (int dd = 0; dd < 8; dd++) {
-          const int vr = 16 * dd + c16, sw = vt_swz(vr);
-          const uint16_t* vrow = &Vt[buf][vr * kVtStride];
-          const uint2 lo = *reinterpret_cast<const uint2*>(vrow + 4 * ((8 * u + q4) ^ sw));
-          const uint2 hi = *reinterpret_cast<const uint2*>(vrow + 4 * ((8 * u + 4 + q4) ^ sw));
-          O[r][dd] = mma32<MT>(make_uint4(lo.x, lo.y, hi.x, hi.y), pb, O[r][dd]);
-        }
+      for (int dd = 0; dd < 8; dd++) {
+        const int vr = 16 * dd + c16, sw = vt_swz(vr);
+        const uint16_t* vrow = &Vt[buf][vr * kVtStride];
+        const uint2 lo = *reinterpret_cast<const uint2*>(vrow + 4 * ((8 * u + q4) ^ sw));
+        const uint2 hi = *reinterpret_cast<const uint2*>(vrow + 4 * ((8 * u + 4 + q4) ^ sw));
+        const uint4 vf = make_uint4(lo.x, lo.y, hi.x, hi.y);
+#pragma unroll
+        for (int r = 0; r < RT; r++) O[r][dd] = mma32<MT>(vf, pb[r][u], O[r][dd]);
       }
     }
   };
 
   const int tfirst = klo & ~(kKT - 1);
-  RawTile A, B;
-  load(tfirst, A);
-  stage(tfirst, A, 0);
-  __syncthreads();
-  int buf = 0;
-  for (int t0 = tfirst; t0 < khi; t0 += kKT) {
-    const bool more = t0 + kKT < khi;
-    if (more) load(t0 + kKT, B);
-    compute(t0, buf);
-    if (more) stage(t0 + kKT, B, buf ^ 1);
+  if constexpr (FMT == KV_Q8) {
+    // s_waitcnt vmcnt(5) (the other slot's five loads of this wave may stay in flight), vmcnt(0), lgkmcnt(0)
+    constexpr int kWaitOne = (0xF << 8) | (0x7 << 4) | 5;
+    constexpr int kWaitAll = (0xF << 8) | (0x7 << 4);
+    constexpr int kWaitLds = (0x3 << 14) | (0x7 << 4) | 0xF;
+    // a workgroup barrier that leaves the other slot's loads in flight (__syncthreads would wait for them)
+    auto barrier = [&]() __attribute__((always_inline)) {
+      __builtin_amdgcn_s_waitcnt(kWaitLds);
+      __builtin_amdgcn_s_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+    };
+    auto step = [&](int t0, uint8_t* S) __attribute__((always_inline)) {
+      if (t0 + kKT < khi) __builtin_amdgcn_s_waitcnt(kWaitOne);
+      else __builtin_amdgcn_s_waitcnt(kWaitAll);
+      barrier();  // the slot's tile is in LDS; every wave is done with the previous tile's operands
+      RawTile T;
+      load_lds(S, T);
+      stage(t0, T, 0);
+      barrier();  // operands ready; the slot is free
+      if (t0 + 2 * kKT < khi) dma(t0 + 2 * kKT, S);
+      compute(t0, 0);
+    };
+    dma(tfirst, raw0);
+    if (tfirst + kKT < khi) dma(tfirst + kKT, raw1);
+    for (int t0 = tfirst;;) {
+      step(t0, raw0);
+      t0 += kKT;
+      if (t0 >= khi) break;
+      step(t0, raw1);
+      t0 += kKT;
+      if (t0 >= khi) break;
+    }
+  } else {
+    RawTile A, B;
+    load(tfirst, A);
+    stage(tfirst, A, 0);
     __syncthreads();
-    buf ^= 1;
+    int buf = 0;
+    for (int t0 = tfirst; t0 < khi; t0 += kKT) {
+      const bool more = t0 + kKT < khi;
+      if (more) load(t0 + kKT, B);
+      compute(t0, buf);
+      if (more) stage(t0 + kKT, B, buf ^ 1);
+      __syncthreads();
+      buf ^= 1;
+    }
   }
 
   // ---- each row's part: m, l (summed over the 4 lanes of the row), o[dims]
@@ -548,13 +629,13 @@ static void launch_fmt(int qdt, int sdt, int rt, dim3 grid, hipStream_t s, hipEv
 
 using namespace lcl;
 
-// Keys a pass-1 workgroup reads: the caller's block, or enough chunks that the grid (about B H L / 64 row blocks
-// times the chunks) fills one resident round of ~512 workgroups -- no more: every extra chunk adds a 520-byte part
-// per row to write and read back.  One chunk (most prefill) writes the output directly.
-static int sdpa_chunk(int block, int B, int H, int L, int N) {
+// Keys a pass-1 workgroup reads: the caller's block, or enough chunks that the grid (about B H L / wg_rows row
+// blocks times the chunks) fills one resident round of ~512 workgroups -- no more: every extra chunk adds a
+// 520-byte part per row to write and read back.  One chunk (most prefill) writes the output directly.
+static int sdpa_chunk(int block, int B, int H, int L, int N, int wg_rows) {
   if (block > 0) return block;
   const int tiles = max(1, (N + kKT - 1) / kKT);
-  const long long rowblocks = max(1LL, ((long long)B * H * L + 63) / 64);
+  const long long rowblocks = max(1LL, ((long long)B * H * L + wg_rows - 1) / wg_rows);
   const int want = int(min((long long)tiles, max(1LL, (512 + rowblocks - 1) / rowblocks)));
   return ((tiles + want - 1) / want) * kKT;
 }
@@ -562,7 +643,7 @@ static int sdpa_chunk(int block, int B, int H, int L, int N) {
 extern "C" {
 
 size_t lcl_sdpa_workspace_bytes(int B, int H, int L, int N, int block) {
-  const int chunk = sdpa_chunk(block, B, H, L, N);
+  const int chunk = sdpa_chunk(block, B, H, L, N, 128);  // 128-row workgroups take the most chunks
   const int nchunks = N > 0 ? (N + chunk - 1) / chunk : 1;
   return nchunks > 1 ? size_t(B) * H * L * nchunks * (2 + kD) * sizeof(float) : 0;
 }
@@ -591,9 +672,13 @@ int lcl_sdpa_ex(const void* q, int qdt, int kvfmt, const uint32_t* kw, const voi
   if (mask_kind == MK_CAUSAL && L > N) return -1;
   if (mask_kind == MK_TREE && (!tree || L > 64 || L > N)) return -2;
   if (mask_kind == MK_DENSE && !dense) return -1;
-  const int chunk = sdpa_chunk(block, B, H, L, N);
+  // row tiles a wave: two (128 rows a workgroup) for 8-bit keys and values when there are more than 64 rows,
+  // halving the dequantization and the operand reads per row; one otherwise (16-bit needs no dequantization)
+  const int rows = L * (H / KVH);
+  const int rt = (kvfmt == KV_Q8 && rows > 64) ? 2 : 1;
+  const int chunk = sdpa_chunk(block, B, H, L, N, 64 * rt);
   const int nchunks = N > 0 ? (N + chunk - 1) / chunk : 1;
-  const size_t need = lcl_sdpa_workspace_bytes(B, H, L, N, block);
+  const size_t need = nchunks > 1 ? size_t(B) * H * L * nchunks * (2 + kD) * sizeof(float) : 0;
   if (need && (!workspace || workspace_bytes < need)) return -3;
   SdpaParams p{};
   p.q = q;
@@ -609,10 +694,6 @@ int lcl_sdpa_ex(const void* q, int qdt, int kvfmt, const uint32_t* kw, const voi
   p.B = B; p.H = H; p.KVH = KVH; p.G = H / KVH; p.L = L; p.N = N; p.cap = cap;
   p.nchunks = nchunks; p.chunk = chunk; p.mask = mask_kind;
   p.direct = nchunks == 1; p.out = out; p.odt = qdt;
-  // one row tile a wave (64 rows a workgroup): two (128 rows) would reuse each staged tile twice as often but
-  // need ~370 registers a lane (one wave a SIMD), which measured slower
-  const int rows = L * p.G;
-  const int rt = 1;
   p.nrowblocks = (rows + 64 * rt - 1) / (64 * rt);
   hipEvent_t e0 = static_cast<hipEvent_t>(ev_start), e1 = static_cast<hipEvent_t>(ev_stop);
   {  // with no key in reach every workgroup records empty parts, so the combine needs no cleared workspace
