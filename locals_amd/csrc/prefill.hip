@@ -142,6 +142,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     head[r] = kvh * p.G + (real[r] ? rowi[r] % p.G : 0);
   }
   const int last_q = min(R - 1, row0 + 64 * RT - 1) / p.G;
+  const int wave_q0 = (row0 + 16 * wave) / p.G;  // the smallest query index among this wave's rows
   const int slo = p.start ? max(p.start[b], 0) : 0;
   const int klo = __builtin_amdgcn_readfirstlane(max(slo, c * p.chunk));
   int khi = min(p.N, (c + 1) * p.chunk);
@@ -173,7 +174,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   __shared__ __attribute__((aligned(16))) uint8_t raw0[FMT == KV_Q8 ? kRawSlot : 16];
   __shared__ __attribute__((aligned(16))) uint8_t raw1[FMT == KV_Q8 ? kRawSlot : 16];
 
-  // Q^T as B operands: qb[r][kk] = q[row][32 kk + 8 q4 + j]
+  // Q^T as B operands: qb[r][kk] = scale log2(e) q[row][32 kk + 8 q4 + j], scaled in fp32 before its one rounding
+  // to the MFMA type, so the products come out as base-2 logits
   uint4 qb[RT][4];
 #pragma unroll
   for (int r = 0; r < RT; r++) {
@@ -182,7 +184,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     for (int kk = 0; kk < 4; kk++) {
       float x[8];
 #pragma unroll
-      for (int j = 0; j < 8; j++) x[j] = ldv<QDT>(p.q, qrow + 32 * kk + 8 * q4 + j);
+      for (int j = 0; j < 8; j++) x[j] = ldv<QDT>(p.q, qrow + 32 * kk + 8 * q4 + j) * p.scale_log2;
       if (!real[r]) {
 #pragma unroll
         for (int j = 0; j < 8; j++) x[j] = 0.0f;
@@ -411,25 +413,37 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         for (int r = 0; r < RT; r++) st[r][t] = mma32<MT>(kf, qb[r][kk], st[r][t]);
       }
     }
+    // a tile every key of which every row of the wave sees needs no mask (for causal prefill, all but the
+    // diagonal tiles); rows past the row count are not written, so they need none either
+    bool full = t0 >= klo && t0 + kKT <= khi;
+    if constexpr (MASK == MK_CAUSAL) full = full && t0 + kKT - 1 <= p.N - p.L + wave_q0;
+    if constexpr (MASK == MK_TREE) full = full && t0 + kKT <= p.N - p.L;
+    if constexpr (MASK == MK_DENSE) full = false;
     uint4 pb[RT][2];  // P^T as B operands: k index 8 q4 + j <-> key 32 u + (j < 4 ? 4 q4 + j : 16 + 4 q4 + j - 4)
 #pragma unroll
     for (int r = 0; r < RT; r++) {
       float tmax = -INFINITY;
+      if (full) {
 #pragma unroll
-      for (int t = 0; t < 4; t++) {
+        for (int t = 0; t < 4; t++)
+          tmax = fmaxf(tmax, fmaxf(fmaxf(st[r][t][0], st[r][t][1]), fmaxf(st[r][t][2], st[r][t][3])));
+      } else {
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-          const int j = t0 + 16 * t + 4 * q4 + i;
-          bool ok = real[r] & (j >= klo) & (j < khi);
-          if constexpr (MASK == MK_CAUSAL) ok = ok & (j <= p.N - p.L + qi[r]);
-          if constexpr (MASK == MK_TREE) {
-            const int d = j - (p.N - p.L);
-            ok = ok & ((d < 0) | (((tbits[r] >> (d & 63)) & 1ull) != 0ull));
+        for (int t = 0; t < 4; t++) {
+#pragma unroll
+          for (int i = 0; i < 4; i++) {
+            const int j = t0 + 16 * t + 4 * q4 + i;
+            bool ok = real[r] & (j >= klo) & (j < khi);
+            if constexpr (MASK == MK_CAUSAL) ok = ok & (j <= p.N - p.L + qi[r]);
+            if constexpr (MASK == MK_TREE) {
+              const int d = j - (p.N - p.L);
+              ok = ok & ((d < 0) | (((tbits[r] >> (d & 63)) & 1ull) != 0ull));
+            }
+            if constexpr (MASK == MK_DENSE) ok = ok & (drow[r][min(max(j, 0), p.N - 1) * p.msk] != 0);
+            const float sc = ok ? st[r][t][i] : -INFINITY;
+            st[r][t][i] = sc;
+            tmax = fmaxf(tmax, sc);
           }
-          if constexpr (MASK == MK_DENSE) ok = ok & (drow[r][min(max(j, 0), p.N - 1) * p.msk] != 0);
-          const float sc = ok ? st[r][t][i] * p.scale_log2 : -INFINITY;
-          st[r][t][i] = sc;
-          tmax = fmaxf(tmax, sc);
         }
       }
       tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
