@@ -1,6 +1,6 @@
 """Benchmark of the batched-attention hot path on one MI355X: 8-bit-KV GQA flash-decode.
 
-    python bench.py [--steps K] [--warmup W] [--config c2|c3|c1] [--cpu-seconds S] [--no-cpu]
+    python bench.py [--steps K] [--warmup W] [--config c2|c3|c4|c5|w1] [--cpu-seconds S] [--no-cpu]
 
 A step is one ``qkv.attend`` over the whole batch (pass 1 + the log-sum-exp combine) with K/V already resident in
 HBM.  Workload (default, "c2"): B=16 rows, 32 query / 8 KV heads, head_dim 128, row contexts n_b ~ U[1024, 32768]
@@ -92,6 +92,10 @@ def config(name: str, seed: int = 0):
         return dict(name="c5", workload="speculative tree verification: 8 rows x 16 draft tokens (random trees, "
                     "branching 1-3, depth <= 8) over 8,192 cached 8-bit keys (BASELINE config 5)", B=8, H=32, KVH=8,
                     L=16, prefix=8192)
+    if name == "w1":
+        return dict(name="w1", workload="sliding-window prompt chunk: 2,048 queries after a ring of 512 keys, window "
+                    "513, Flint's 32 query / 4 KV heads, bf16 K/V (the banded attention, locals/fuse.py:113-125)",
+                    B=1, H=32, KVH=4, L=2048, prefix=512, window=513)
     raise SystemExit(f"unknown config {name}")
 
 
@@ -124,8 +128,8 @@ def random_tree(g, L=16, max_depth=8):
 
 
 def bench_multi(cfg, args, dev):
-    """C4 (decode rows + causal prefill chunk) and C5 (tree verification): pass-1 times from the dispatch events,
-    FLOPs and bytes from the shapes."""
+    """C4 (decode rows + causal prefill chunk), C5 (tree verification) and W1 (sliding-window chunk over 16-bit K/V):
+    pass-1 times from the dispatch events, FLOPs and bytes from the shapes."""
     import torch
 
     from locals_amd import _lib, qkv, sdpa
@@ -138,8 +142,15 @@ def bench_multi(cfg, args, dev):
     Bp = 1 if cfg["name"] == "c4" else cfg["B"]
     N = P + L
     cap = (N + 255) // 256 * 256
+    W = cfg.get("window", 0)
     sets = []
     for s in range(args.sets):
+        if W:  # 16-bit K/V, the rotating cache's dtype
+            K = torch.randn((Bp, KVH, cap, 128), generator=gen, device=dev, dtype=torch.bfloat16)
+            V = torch.randn((Bp, KVH, cap, 128), generator=gen, device=dev, dtype=torch.bfloat16)
+            q = torch.randn((Bp, H, L, 128), generator=gen, device=dev, dtype=torch.bfloat16)
+            sets.append((q, K, V))
+            continue
         K = qkv._zeros(Bp, KVH, cap, 128, torch.float16, dev)
         V = qkv._zeros(Bp, KVH, cap, 128, torch.float16, dev)
         for b in range(Bp):
@@ -161,22 +172,30 @@ def bench_multi(cfg, args, dev):
         mask = sdpa.TreeMask.from_local(torch.from_numpy(local), device=dev)
         mk, tree, tree_bs = 2, mask.bits, L
         pairs = int(Bp * (L * P + local.sum()))
+    elif W:
+        mk, tree, tree_bs = 4, None, 0
+        pairs = Bp * sum(min(W, P + i + 1) for i in range(L))
     else:
         mk, tree, tree_bs = 1, None, 0
         pairs = sum(P + i + 1 for i in range(L))
     flops = pairs * H * 4 * 128
-    kv_bytes = Bp * KVH * N * 272
+    kv_bytes = Bp * KVH * N * (512 if W else 272)
     nbytes = int(lib.lcl_sdpa_workspace_bytes(Bp, H, L, N, sdpa.BLOCK))
     ws = torch.empty(nbytes // 4 + 1, dtype=torch.float32, device=dev)
-    out = torch.empty((Bp, H, L, 128), dtype=torch.float16, device=dev)
+    out = torch.empty((Bp, H, L, 128), dtype=torch.bfloat16 if W else torch.float16, device=dev)
     ev = Events(2 * args.steps + 2)
     P_ = _lib.ptr
 
     def run(i, e0=None, e1=None):
         q, K, V = sets[i % len(sets)]
-        rc = lib.lcl_sdpa_ex(P_(q), 0, 0, P_(K[0]), P_(K[1]), P_(K[2]), P_(V[0]), P_(V[1]), P_(V[2]), None, None, 0,
-                             None, mk, P_(tree), tree_bs, None, 0, 0, 0, 0, None, float(1 / np.sqrt(128)), Bp, H, KVH,
-                             L, N, 128, cap, sdpa.BLOCK, P_(out), P_(ws), nbytes, stream, e0, e1)
+        if W:
+            rc = lib.lcl_sdpa_ex(P_(q), 1, 1, None, None, None, None, None, None, P_(K), P_(V), 1, None, mk, W, None,
+                                 0, None, 0, 0, 0, 0, None, float(1 / np.sqrt(128)), Bp, H, KVH, L, N, 128, cap,
+                                 sdpa.BLOCK, P_(out), P_(ws), nbytes, stream, e0, e1)
+        else:
+            rc = lib.lcl_sdpa_ex(P_(q), 0, 0, P_(K[0]), P_(K[1]), P_(K[2]), P_(V[0]), P_(V[1]), P_(V[2]), None, None,
+                                 0, None, mk, 0, P_(tree), tree_bs, None, 0, 0, 0, 0, None, float(1 / np.sqrt(128)), Bp,
+                                 H, KVH, L, N, 128, cap, sdpa.BLOCK, P_(out), P_(ws), nbytes, stream, e0, e1)
         _lib.check(rc, "lcl_sdpa_ex")
 
     for i in range(args.warmup):
@@ -193,6 +212,8 @@ def bench_multi(cfg, args, dev):
            "kv_GBs": round(kv_bytes / (us * 1e-6) / 1e9, 1), "flops": flops, "kv_bytes": kv_bytes}
     if cfg["name"] == "c5":
         res["trees"] = trees
+    if W:
+        res["window"] = W
     return res
 
 
@@ -312,14 +333,15 @@ def main():
     cfg = config(args.config)
     if args.block is not None:
         qkv.BLOCK = args.block
-    if cfg["name"] in ("c4", "c5"):
+    if cfg["name"] in ("c4", "c5", "w1"):
         from locals_amd import sdpa
 
         if args.block is not None:
             sdpa.BLOCK = args.block
         multi = bench_multi(cfg, args, dev)
-        if cfg["name"] == "c5":
-            print(json.dumps({"config": cfg["workload"], "tree_verify": multi}), flush=True)
+        if cfg["name"] in ("c5", "w1"):
+            key = "tree_verify" if cfg["name"] == "c5" else "window_prefill"
+            print(json.dumps({"config": cfg["workload"], key: multi}), flush=True)
             return
         cfg = dict(cfg, workload=cfg["workload"])  # the decode rows below; the prefill part reported beside them
     sets, start, n, cap = build_sets(cfg, args.sets, dev)

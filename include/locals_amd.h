@@ -104,11 +104,16 @@ size_t lcl_sdpa_workspace_bytes(int B, int H, int L, int N, int block);
  *   mask_kind 0 none; 1 causal (query i sees key j iff j <= N - L + i);
  *   2 tree: key j < N - L visible to all, key N - L + d visible to query i iff
  *     bit d of tree[b * tree_bs + i] (L <= 64; tree_bs = L, or 0 for one shared mask);
- *   3 dense: uint8 dense[b*msb + h*msh + i*msq + j*msk] != 0 (strides may be 0)
+ *   3 dense: uint8 dense[b*msb + h*msh + i*msq + j*msk] != 0 (strides may be 0);
+ *   4 sliding window: query i sees key j iff N - L + i - window < j <= N - L + i
+ *     (window >= 1; the banded prompt chunks of the sliding-window layers,
+ *     locals/fuse.py:113-125, locals/models/flint_streamed.py:114-128); each
+ *     workgroup reads only the keys its queries' windows reach
+ *   window is read for mask_kind 4 only.
  *   sinks (H,) float32 or NULL.  A query with no visible key and no sink gives 0. */
 int lcl_sdpa(const void* q, int qdt, int kvfmt, const uint32_t* kw, const void* ks, const void* kb,
              const uint32_t* vw, const void* vs, const void* vb, const void* kf, const void* vf, int kvdt,
-             const int32_t* start, int mask_kind, const unsigned long long* tree, long long tree_bs,
+             const int32_t* start, int mask_kind, int window, const unsigned long long* tree, long long tree_bs,
              const uint8_t* dense, long long msb, long long msh, long long msq, long long msk, const float* sinks,
              float scale, int B, int H, int KVH, int L, int N, int head_dim, int cap, int block, void* out,
              void* workspace, size_t workspace_bytes, void* stream);
@@ -117,7 +122,7 @@ int lcl_sdpa(const void* q, int qdt, int kvfmt, const uint32_t* kw, const void* 
  * counterpart in the reference. */
 int lcl_sdpa_ex(const void* q, int qdt, int kvfmt, const uint32_t* kw, const void* ks, const void* kb,
                 const uint32_t* vw, const void* vs, const void* vb, const void* kf, const void* vf, int kvdt,
-                const int32_t* start, int mask_kind, const unsigned long long* tree, long long tree_bs,
+                const int32_t* start, int mask_kind, int window, const unsigned long long* tree, long long tree_bs,
                 const uint8_t* dense, long long msb, long long msh, long long msq, long long msk, const float* sinks,
                 float scale, int B, int H, int KVH, int L, int N, int head_dim, int cap, int block, void* out,
                 void* workspace, size_t workspace_bytes, void* stream, void* ev_start, void* ev_stop);

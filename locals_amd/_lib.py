@@ -34,9 +34,9 @@ SIGNATURES = {
     "lcl_quantize_append": (I, [P, P, I, P, P, P, P, P, P, I, I, I, I, I, I, I, P]),
     "lcl_dequantize": (I, [P, P, P, I, ctypes.c_longlong, I, P, I, P]),
     "lcl_sdpa_workspace_bytes": (Z, [I, I, I, I, I]),
-    "lcl_sdpa": (I, [P, I, I, P, P, P, P, P, P, P, P, I, P, I, P, LL, P, LL, LL, LL, LL, P, F, I, I, I, I, I, I, I, I,
+    "lcl_sdpa": (I, [P, I, I, P, P, P, P, P, P, P, P, I, P, I, I, P, LL, P, LL, LL, LL, LL, P, F, I, I, I, I, I, I, I, I,
                      P, P, Z, P]),
-    "lcl_sdpa_ex": (I, [P, I, I, P, P, P, P, P, P, P, P, I, P, I, P, LL, P, LL, LL, LL, LL, P, F, I, I, I, I, I, I, I,
+    "lcl_sdpa_ex": (I, [P, I, I, P, P, P, P, P, P, P, P, I, P, I, I, P, LL, P, LL, LL, LL, LL, P, F, I, I, I, I, I, I, I,
                         I, P, P, Z, P, P, P]),
     "lcl_qk_norm_rope": (I, [P, I, P, P, P, I, F, F, I, I, I, I, I, I, P, P, P, P]),
     "lcl_qk_norm_rope_append": (I, [P, I, P, P, P, I, F, F, I, I, I, I, I, I, P, P, P, P, P, P, P, I, I, I, P]),

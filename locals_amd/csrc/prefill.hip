@@ -8,6 +8,9 @@
 //  * tree verification: prefix visible to every new token, ancestor-only within the
 //    new tokens (locals/treedec.py:56-79, locals/packed.py:107-116,161-182);
 //  * any boolean array mask (locals/fuse.py:139, tests/test_flint.py:534-552);
+//  * the sliding-window layers' prompt chunks (locals/fuse.py:113-125, locals/models/flint_streamed.py:114-128):
+//    causal within a window of W keys, query i (position N - L + i) seeing keys (N - L + i - W, N - L + i];
+//    the reference slices the keys a band of queries reaches, here each workgroup reads only its rows' band;
 //  * the sink is a logit in the denominator only.
 //
 // MI355X design.  Grid (key chunk, row block, row x kv head); a workgroup = 4 waves =
@@ -46,7 +49,7 @@ constexpr float kThr = 6.0f;
 // consecutive rows a thread and rows 8 apart across a wave's lanes, then fall in distinct banks
 __device__ __forceinline__ int vt_swz(int d) { return (d >> 3) & 15; }
 
-enum MaskKind { MK_NONE = 0, MK_CAUSAL = 1, MK_TREE = 2, MK_DENSE = 3 };
+enum MaskKind { MK_NONE = 0, MK_CAUSAL = 1, MK_TREE = 2, MK_DENSE = 3, MK_WINDOW = 4 };
 enum KvFmt { KV_Q8 = 0, KV_16 = 1 };
 
 struct SdpaParams {
@@ -70,6 +73,7 @@ struct SdpaParams {
   float* po;
   float scale_log2;
   int B, H, KVH, G, L, N, cap, nchunks, chunk, nrowblocks, mask;
+  int window;  // MK_WINDOW: keys a query sees, itself included
   void* out;  // direct: one chunk covers every key, so pass 1 writes the normalized output (B, H, L, 128), dtype odt
   int direct, odt;
 };
@@ -144,10 +148,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const int last_q = min(R - 1, row0 + 64 * RT - 1) / p.G;
   const int wave_q0 = (row0 + 16 * wave) / p.G;  // the smallest query index among this wave's rows
   const int slo = p.start ? max(p.start[b], 0) : 0;
-  const int klo = __builtin_amdgcn_readfirstlane(max(slo, c * p.chunk));
-  int khi = min(p.N, (c + 1) * p.chunk);
-  if constexpr (MASK == MK_CAUSAL) khi = min(khi, p.N - p.L + last_q + 1);
-  khi = __builtin_amdgcn_readfirstlane(khi);
+  // keys the workgroup's rows can see: [blo, bhi); chunks are counted from base (the band's first tile for a
+  // window, key 0 otherwise)
+  int blo = slo, bhi = p.N, base = 0;
+  if constexpr (MASK == MK_CAUSAL || MASK == MK_WINDOW) bhi = min(bhi, p.N - p.L + last_q + 1);
+  if constexpr (MASK == MK_WINDOW) {
+    blo = max(blo, p.N - p.L + row0 / p.G - p.window + 1);
+    base = max(blo, 0) & ~(kKT - 1);
+  }
+  const int klo = __builtin_amdgcn_readfirstlane(max(blo, base + c * p.chunk));
+  const int khi = __builtin_amdgcn_readfirstlane(min(bhi, base + (c + 1) * p.chunk));
   if (klo >= khi) {  // uniform: nothing here; rows record an empty part (or, direct, a zero output)
 #pragma unroll
     for (int r = 0; r < RT; r++) {
@@ -418,6 +428,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     bool full = t0 >= klo && t0 + kKT <= khi;
     if constexpr (MASK == MK_CAUSAL) full = full && t0 + kKT - 1 <= p.N - p.L + wave_q0;
     if constexpr (MASK == MK_TREE) full = full && t0 + kKT <= p.N - p.L;
+    if constexpr (MASK == MK_WINDOW)  // causal for the wave's first query, in the window of its last
+      full = full && t0 + kKT - 1 <= p.N - p.L + wave_q0 &&
+             t0 > p.N - p.L + (row0 + 64 * (RT - 1) + 16 * wave + 15) / p.G - p.window;
     if constexpr (MASK == MK_DENSE) full = false;
     uint4 pb[RT][2];  // P^T as B operands: k index 8 q4 + j <-> key 32 u + (j < 4 ? 4 q4 + j : 16 + 4 q4 + j - 4)
 #pragma unroll
@@ -435,6 +448,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             const int j = t0 + 16 * t + 4 * q4 + i;
             bool ok = real[r] & (j >= klo) & (j < khi);
             if constexpr (MASK == MK_CAUSAL) ok = ok & (j <= p.N - p.L + qi[r]);
+            if constexpr (MASK == MK_WINDOW) {
+              const int pos = p.N - p.L + qi[r];
+              ok = ok & (j <= pos) & (j > pos - p.window);
+            }
             if constexpr (MASK == MK_TREE) {
               const int d = j - (p.N - p.L);
               ok = ok & ((d < 0) | (((tbits[r] >> (d & 63)) & 1ull) != 0ull));
@@ -455,13 +472,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
         for (int dd = 0; dd < 8; dd++) O[r][dd] *= corr;
       }
+      // a row that has seen no key yet (m_run -inf) has only -inf scores here: exp2(-inf - 0) = 0
+      const float msub = m_run[r] == -INFINITY ? 0.0f : m_run[r];
       uint32_t pw[4][2];
 #pragma unroll
       for (int t = 0; t < 4; t++) {
         float pv[4];
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-          pv[i] = fast_exp2(st[r][t][i] - m_run[r]);  // -inf -> 0
+          pv[i] = fast_exp2(st[r][t][i] - msub);  // -inf -> 0
           l_acc[r] += pv[i];
         }
         pw[t][0] = pack2<MT>(pv[0], pv[1]);
@@ -609,9 +628,15 @@ __global__ __launch_bounds__(256) void sdpa_combine(SdpaCombineParams p) {
 
 template <int QDT, int SDT, int FMT, int MT, int MASK>
 static void launch_rt(int rt, dim3 grid, hipStream_t s, hipEvent_t e0, hipEvent_t e1, const SdpaParams& p) {
-  (void)rt;
-  if (rt == 2) hipExtLaunchKernelGGL((sdpa_pass1<QDT, SDT, FMT, MT, MASK, 2>), grid, dim3(256), 0, s, e0, e1, 0, p);
-  else hipExtLaunchKernelGGL((sdpa_pass1<QDT, SDT, FMT, MT, MASK, 1>), grid, dim3(256), 0, s, e0, e1, 0, p);
+  // two row tiles only for 8-bit keys and values under masks read per key pair or none (a dense mask's byte loads
+  // for two tiles would not fit in registers)
+  if constexpr (FMT == KV_Q8 && MASK != MK_DENSE) {
+    if (rt == 2) {
+      hipExtLaunchKernelGGL((sdpa_pass1<QDT, SDT, FMT, MT, MASK, 2>), grid, dim3(256), 0, s, e0, e1, 0, p);
+      return;
+    }
+  }
+  hipExtLaunchKernelGGL((sdpa_pass1<QDT, SDT, FMT, MT, MASK, 1>), grid, dim3(256), 0, s, e0, e1, 0, p);
 }
 
 template <int QDT, int SDT, int FMT, int MT>
@@ -620,6 +645,7 @@ static void launch_mask(int rt, dim3 grid, hipStream_t s, hipEvent_t e0, hipEven
     case MK_CAUSAL: launch_rt<QDT, SDT, FMT, MT, MK_CAUSAL>(rt, grid, s, e0, e1, p); break;
     case MK_TREE: launch_rt<QDT, SDT, FMT, MT, MK_TREE>(rt, grid, s, e0, e1, p); break;
     case MK_DENSE: launch_rt<QDT, SDT, FMT, MT, MK_DENSE>(rt, grid, s, e0, e1, p); break;
+    case MK_WINDOW: launch_rt<QDT, SDT, FMT, MT, MK_WINDOW>(rt, grid, s, e0, e1, p); break;
     default: launch_rt<QDT, SDT, FMT, MT, MK_NONE>(rt, grid, s, e0, e1, p); break;
   }
 }
@@ -664,7 +690,7 @@ size_t lcl_sdpa_workspace_bytes(int B, int H, int L, int N, int block) {
 
 int lcl_sdpa_ex(const void* q, int qdt, int kvfmt, const uint32_t* kw, const void* ks, const void* kb,
                 const uint32_t* vw, const void* vs, const void* vb, const void* kf, const void* vf, int kvdt,
-                const int32_t* start, int mask_kind, const unsigned long long* tree, long long tree_bs,
+                const int32_t* start, int mask_kind, int window, const unsigned long long* tree, long long tree_bs,
                 const uint8_t* dense, long long msb, long long msh, long long msq, long long msk, const float* sinks,
                 float scale, int B, int H, int KVH, int L, int N, int head_dim, int cap, int block, void* out,
                 void* workspace, size_t workspace_bytes, void* stream_, void* ev_start, void* ev_stop) {
@@ -682,16 +708,25 @@ int lcl_sdpa_ex(const void* q, int qdt, int kvfmt, const uint32_t* kw, const voi
   } else {
     return -1;
   }
-  if (mask_kind < MK_NONE || mask_kind > MK_DENSE) return -1;
-  if (mask_kind == MK_CAUSAL && L > N) return -1;
+  if (mask_kind < MK_NONE || mask_kind > MK_WINDOW) return -1;
+  if ((mask_kind == MK_CAUSAL || mask_kind == MK_WINDOW) && L > N) return -1;
+  if (mask_kind == MK_WINDOW && window <= 0) return -1;
   if (mask_kind == MK_TREE && (!tree || L > 64 || L > N)) return -2;
   if (mask_kind == MK_DENSE && !dense) return -1;
   // row tiles a wave: two (128 rows a workgroup) for 8-bit keys and values when there are more than 64 rows,
-  // halving the dequantization and the operand reads per row; one otherwise (16-bit needs no dequantization)
+  // halving the dequantization and the operand reads per row; one otherwise (16-bit needs no dequantization; a
+  // dense mask's per-row byte reads would not fit beside two tiles' registers)
   const int rows = L * (H / KVH);
-  const int rt = (kvfmt == KV_Q8 && rows > 64) ? 2 : 1;
-  const int chunk = sdpa_chunk(block, B, H, L, N, 64 * rt);
-  const int nchunks = N > 0 ? (N + chunk - 1) / chunk : 1;
+  const int rt = (kvfmt == KV_Q8 && mask_kind != MK_DENSE && rows > 64) ? 2 : 1;
+  int chunk = sdpa_chunk(block, B, H, L, N, 64 * rt);
+  int nchunks = N > 0 ? (N + chunk - 1) / chunk : 1;
+  if (mask_kind == MK_WINDOW && N > 0) {
+    // a workgroup's band spans at most the window, its rows' queries and the alignment of its first tile; a
+    // chunk no shorter than the unwindowed one keeps the chunk count within lcl_sdpa_workspace_bytes
+    const long long ext = min((long long)N, (long long)window + (64 * rt - 1) / (H / KVH) + kKT);
+    chunk = max(chunk, sdpa_chunk(block, B, H, L, int(ext), 64 * rt));
+    nchunks = int((ext + chunk - 1) / chunk);
+  }
   const size_t need = nchunks > 1 ? size_t(B) * H * L * nchunks * (2 + kD) * sizeof(float) : 0;
   if (need && (!workspace || workspace_bytes < need)) return -3;
   SdpaParams p{};
@@ -706,7 +741,7 @@ int lcl_sdpa_ex(const void* q, int qdt, int kvfmt, const uint32_t* kw, const voi
   p.pm = ws; p.pl = ws + np; p.po = ws + 2 * np;
   p.scale_log2 = scale * kLog2e;
   p.B = B; p.H = H; p.KVH = KVH; p.G = H / KVH; p.L = L; p.N = N; p.cap = cap;
-  p.nchunks = nchunks; p.chunk = chunk; p.mask = mask_kind;
+  p.nchunks = nchunks; p.chunk = chunk; p.mask = mask_kind; p.window = window;
   p.direct = nchunks == 1; p.out = out; p.odt = qdt;
   p.nrowblocks = (rows + 64 * rt - 1) / (64 * rt);
   hipEvent_t e0 = static_cast<hipEvent_t>(ev_start), e1 = static_cast<hipEvent_t>(ev_stop);
@@ -724,11 +759,11 @@ int lcl_sdpa_ex(const void* q, int qdt, int kvfmt, const uint32_t* kw, const voi
 
 int lcl_sdpa(const void* q, int qdt, int kvfmt, const uint32_t* kw, const void* ks, const void* kb,
              const uint32_t* vw, const void* vs, const void* vb, const void* kf, const void* vf, int kvdt,
-             const int32_t* start, int mask_kind, const unsigned long long* tree, long long tree_bs,
+             const int32_t* start, int mask_kind, int window, const unsigned long long* tree, long long tree_bs,
              const uint8_t* dense, long long msb, long long msh, long long msq, long long msk, const float* sinks,
              float scale, int B, int H, int KVH, int L, int N, int head_dim, int cap, int block, void* out,
              void* workspace, size_t workspace_bytes, void* stream) {
-  return lcl_sdpa_ex(q, qdt, kvfmt, kw, ks, kb, vw, vs, vb, kf, vf, kvdt, start, mask_kind, tree, tree_bs, dense, msb,
+  return lcl_sdpa_ex(q, qdt, kvfmt, kw, ks, kb, vw, vs, vb, kf, vf, kvdt, start, mask_kind, window, tree, tree_bs, dense, msb,
                      msh, msq, msk, sinks, scale, B, H, KVH, L, N, head_dim, cap, block, out, workspace,
                      workspace_bytes, stream, nullptr, nullptr);
 }

@@ -9,7 +9,8 @@ place, dequantized in LDS by ``lcl_sdpa``).
 
 Masks: ``None``; ``"causal"`` (the last query aligned with the last key, locals/fuse.py:131-137); a boolean tensor
 broadcastable to (B, H, L, N); or a ``TreeMask`` (the prefix visible to every new token, ancestor-only within the
-new tokens, locals/treedec.py:56-67) which the kernel reads as one 64-bit word a query.  ``sinks`` (H,) are logits
+new tokens, locals/treedec.py:56-67) which the kernel reads as one 64-bit word a query; or a ``WindowMask`` (the
+sliding-window layers' mask: causal within the last W keys, locals/fuse.py:113-125).  ``sinks`` (H,) are logits
 in the denominator only.
 """
 
@@ -24,7 +25,19 @@ from .qkv import _words_ok
 
 BLOCK = 0  # keys a pass-1 workgroup reads (a multiple of 64); 0: the library's choice
 
-MASK_NONE, MASK_CAUSAL, MASK_TREE, MASK_DENSE = 0, 1, 2, 3
+MASK_NONE, MASK_CAUSAL, MASK_TREE, MASK_DENSE, MASK_WINDOW = 0, 1, 2, 3, 4
+
+
+class WindowMask:
+    """The mask a sliding-window layer gives a prompt chunk (mlx-lm's ``create_causal_mask(..., window_size=W)``
+    for a ``RotatingKVCache``, locals/models/flint.py:157,197): query i of L, at position N - L + i, sees the keys
+    (N - L + i - W, N - L + i].  The reference computes it as bands of queries over the keys each band reaches
+    (locals/fuse.py:113-125, locals/models/flint_streamed.py:114-128); the kernel reads each workgroup's band."""
+
+    def __init__(self, window: int):
+        if int(window) < 1:
+            raise ValueError("a window holds at least the query's own key")
+        self.window = int(window)
 
 
 class TreeMask:
@@ -138,7 +151,7 @@ def scaled_dot_product_attention(q: torch.Tensor, k, v, *, scale: float, mask=No
         raise ValueError("q and k/v disagree on rows or heads")
     dev = _lib.require_gpu(q, *tensors, sinks, start)
     q = q.contiguous()
-    mk, tree, tree_bs, dense, strides = MASK_NONE, None, 0, None, (0, 0, 0, 0)
+    mk, window, tree, tree_bs, dense, strides = MASK_NONE, 0, None, 0, None, (0, 0, 0, 0)
     if mask is None:
         pass
     elif isinstance(mask, str):
@@ -152,6 +165,10 @@ def scaled_dot_product_attention(q: torch.Tensor, k, v, *, scale: float, mask=No
             raise ValueError("TreeMask must cover the L queries, one row or one for all")
         mk, tree = MASK_TREE, mask.bits.to(dev)
         tree_bs = L if mask.bits.shape[0] == B and B > 1 else 0
+    elif isinstance(mask, WindowMask):
+        if L > N:
+            raise ValueError("a window mask needs at least as many keys as queries")
+        mk, window = MASK_WINDOW, mask.window
     elif isinstance(mask, torch.Tensor):
         if mask.dtype != torch.bool:
             raise ValueError("array masks must be boolean (additive masks are not part of the reference's calls)")
@@ -163,7 +180,7 @@ def scaled_dot_product_attention(q: torch.Tensor, k, v, *, scale: float, mask=No
         strides = tuple(dense.stride())
         mk = MASK_DENSE
     else:
-        raise ValueError("mask must be None, 'causal', a boolean tensor or a TreeMask")
+        raise ValueError("mask must be None, 'causal', a boolean tensor, a TreeMask or a WindowMask")
     sk = None if sinks is None else sinks.to(device=dev, dtype=torch.float32).reshape(-1).contiguous()
     if sk is not None and sk.numel() != H:
         raise ValueError("sinks must have one entry a query head")
@@ -175,7 +192,7 @@ def scaled_dot_product_attention(q: torch.Tensor, k, v, *, scale: float, mask=No
     out = torch.empty((B, H, L, D), dtype=q.dtype, device=dev)
     P = _lib.ptr
     rc = lib.lcl_sdpa(P(q), _lib.dtype_code(q.dtype), fmt, P(kw), P(ks), P(kb), P(vw), P(vs), P(vb), P(kf), P(vf),
-                      _lib.dtype_code(kvdt), P(st), mk, P(tree), tree_bs, P(dense), *strides, P(sk), float(scale),
+                      _lib.dtype_code(kvdt), P(st), mk, window, P(tree), tree_bs, P(dense), *strides, P(sk), float(scale),
                       B, H, KVH, L, N, D, cap, blk, P(out), P(ws), nbytes, _lib.stream_of(dev))
     _lib.check(rc, "lcl_sdpa")
     return out

@@ -68,6 +68,32 @@ def causal_mask(L: int, N: int) -> np.ndarray:
     return np.arange(N)[None, :] <= (N - L + np.arange(L))[:, None]
 
 
+def window_mask(L: int, N: int, W: int) -> np.ndarray:
+    """A sliding-window layer's mask over a prompt chunk (mlx-lm's create_causal_mask with window_size W, as a
+    RotatingKVCache layer gets it, locals/models/flint.py:157): (L, N) bool, query i at position N - L + i sees key
+    j iff N - L + i - W < j <= N - L + i.  The lower bound is the one the reference's band slicing assumes
+    (locals/fuse.py:122: a band's first query reaches back W - 1 keys)."""
+    pos = (N - L + np.arange(L))[:, None]
+    j = np.arange(N)[None, :]
+    return (j <= pos) & (j > pos - W)
+
+
+def banded_sdpa(q, k, v, scale: float, W: int, sinks=None, band: int = 512, dtype: str = "float16") -> np.ndarray:
+    """``FusedFlintAttention._banded`` (locals/fuse.py:113-125): the chunk's L queries (the last L of the N keys) in
+    bands of ``band``, each band attending over the slice of keys its window reaches, with the matching slice of
+    the window mask; the bands' outputs concatenated along the queries."""
+    L, N = np.shape(q)[2], np.shape(k)[2]
+    P = N - L
+    mask = window_mask(L, N, W)
+    outs = []
+    for a in range(0, L, band):
+        b = min(L, a + band)
+        lo, hi = max(0, P + a - (W - 1)), P + b
+        outs.append(sdpa(q[:, :, a:b], k[:, :, lo:hi], v[:, :, lo:hi], scale, mask[a:b, lo:hi][None, None], sinks,
+                         dtype))
+    return np.concatenate(outs, axis=2)
+
+
 def branch_mask(br) -> np.ndarray:
     """The reference's tree mask over the new tokens (locals/treedec.py:56-67, locals/packed.py:176-181):
     token i sees token j iff j <= i and (same branch or j on the main path, br[j] < 0)."""

@@ -78,6 +78,11 @@ def test_entry_points_reject_bad_arguments_without_a_gpu():
     rc = lib.lcl_qk_norm_rope_append(one, 0, one, one, one, 0, 1e-6, 13.3, 1, 1, 5, 4, 2, 128, one, one, one, one,
                                      one, one, one, 256, 0, 2, None)
     assert rc == -1  # round mode
+    # lcl_sdpa: the sliding window needs window >= 1 and L <= N; unknown mask kinds are invalid
+    sd = lambda mk, W, L=4, N=10: lib.lcl_sdpa(one, 0, 1, None, None, None, None, None, None, one, one, 0, None, mk,
+                                              W, None, 0, None, 0, 0, 0, 0, None, 0.1, 1, 8, 2, L, N, 128, 16, 0, one,
+                                              None, 0, None)
+    assert sd(4, 0) == -1 and sd(4, -3) == -1 and sd(4, 5, L=11) == -1 and sd(5, 5) == -1
 
 
 def test_python_wrappers_refuse_cpu_tensors():

@@ -4,7 +4,9 @@ Cases: the chunked-prefill shape (causal over an 8-bit prefix, the last query al
 locals/fuse.py:131-137), tree verification (prefix visible, ancestor-only among the new tokens,
 locals/treedec.py:56-67), dense boolean masks (locals/fuse.py:139), sinks, left padding, fp16 and bf16, and the
 reference's invariants: a chunk equals decoding its tokens one by one (tests/test_flint.py:420-455), a chain tree
-equals the causal mask, 5 to 8 queries unpadded equal the reference's padded pass (tests/test_flint.py:534-552).
+equals the causal mask, 5 to 8 queries unpadded equal the reference's padded pass (tests/test_flint.py:534-552);
+the sliding-window mask of the banded prompt chunks (locals/fuse.py:113-125) over 16-bit and 8-bit K/V, with left
+padding; a query with no visible key gives 0.
 Bars: 2e-3 max-abs for fp16 outputs; bf16 2^-7 (1 + max|ref|) (tests/test_flint.py:295).
 """
 
@@ -205,3 +207,75 @@ def test_qkv_attention_prompt_branch(dev):
     V = oq.quantize(np.concatenate([v0, v1], 2))
     ref = oa.sdpa_q8(q, K, V, 0.0884, "causal", sinks)
     assert np.abs(_np(out) - ref).max() <= 2e-3
+
+
+@pytest.mark.parametrize("kvdt", ["float16", "bfloat16"])
+@pytest.mark.parametrize("W", [1, 37, 129, 513, 100000])
+def test_window_16bit(dev, kvdt, W):
+    """A sliding-window layer's prompt chunk (fuse.banded, the reference's _banded, locals/fuse.py:113-125) over
+    16-bit K/V: Flint's head ratio (G = 8), the chunk after a ring of 512 earlier keys; windows from the query alone
+    to wider than every key (then the causal mask)."""
+    from locals_amd import fuse
+
+    print(f"window 16-bit W={W} {kvdt}", flush=True)
+    g = rng(30 + W)
+    B, H, KVH, L, N = 1, 16, 2, 300, 812
+    q = normal16(g, (B, H, L, 128), dtype=kvdt)
+    k = normal16(g, (B, KVH, N, 128), dtype=kvdt)
+    v = normal16(g, (B, KVH, N, 128), dtype=kvdt)
+    sinks = normal16(g, (H,), 1.0, dtype=kvdt)
+    got = fuse.banded(to_torch(q, dev, kvdt), to_torch(k, dev, kvdt), to_torch(v, dev, kvdt), W, 0.09,
+                      to_torch(sinks, dev, kvdt))
+    torch.cuda.synchronize()
+    f = lambda a: oq.to_f32(a, kvdt)  # noqa: E731
+    ref = oa.sdpa(f(q), f(k), f(v), 0.09, oa.window_mask(L, N, W)[None, None], f(sinks), dtype="float64")
+    assert np.abs(_np(got) - ref).max() <= _tol(ref, kvdt)
+
+
+@pytest.mark.parametrize("W", [7, 100, 700])
+def test_window_q8_left_padded(dev, W):
+    """The window over 8-bit K/V (two row tiles a wave), with left padding: row 2's first queries have their whole
+    window before its start and give 0; sinks present."""
+    from locals_amd.sdpa import WindowMask, scaled_dot_product_attention
+
+    print(f"window q8 W={W}", flush=True)
+    g = rng(40 + W)
+    B, H, KVH, L, N, cap = 3, 32, 4, 64, 700, 768
+    q = normal16(g, (B, H, L, 128))
+    K, V = q8_cache(g, B, KVH, cap)
+    sinks = normal16(g, (H,), 2.0)
+    start = np.array([0, 17, 690], np.int32)
+    Kt, Vt = triple_to_torch(K, dev), triple_to_torch(V, dev)
+    got = scaled_dot_product_attention(to_torch(q, dev), tuple(a[:, :, :N] for a in Kt),
+                                       tuple(a[:, :, :N] for a in Vt), scale=0.0884, mask=WindowMask(W),
+                                       sinks=to_torch(sinks, dev), start=to_torch(start, dev))
+    torch.cuda.synchronize()
+    vis = oa.window_mask(L, N, W)[None, None] & (np.arange(N)[None, None, None, :] >= start[:, None, None, None])
+    ref = oa.sdpa_q8(q, K, V, 0.0884, vis, sinks, n=N)
+    assert np.abs(_np(got) - ref).max() <= 2e-3
+    blind = ~vis[2, 0].any(-1)  # row 2's queries that see no key
+    assert blind.any() and not np.abs(_np(got)[2][:, blind]).any()
+
+
+def test_query_with_no_visible_key_is_zero(dev):
+    """A query whose mask row is all false gives 0, sink or not, in every chunking (with one chunk pass 1 writes
+    the output itself)."""
+    from locals_amd.sdpa import scaled_dot_product_attention
+
+    g = rng(13)
+    B, H, KVH, L, N = 2, 8, 2, 6, 150
+    q = normal16(g, (B, H, L, 128))
+    k = normal16(g, (B, KVH, N, 128))
+    v = normal16(g, (B, KVH, N, 128))
+    vis = g.random((B, 1, L, N)) < 0.3
+    vis[:, :, 2] = False
+    vis[1, :, 4] = False
+    for sinks in (None, normal16(g, (H,), 1.0)):
+        got = scaled_dot_product_attention(to_torch(q, dev), to_torch(k, dev), to_torch(v, dev), scale=0.1,
+                                           mask=torch.from_numpy(vis).to(dev),
+                                           sinks=None if sinks is None else to_torch(sinks, dev))
+        torch.cuda.synchronize()
+        out = _np(got)
+        assert not np.abs(out[:, :, 2]).any() and not np.abs(out[1, :, 4]).any()
+        ref = oa.sdpa(q, k, v, 0.1, vis, sinks, dtype="float16")
+        assert np.abs(out - ref).max() <= 2e-3

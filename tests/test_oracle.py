@@ -5,7 +5,8 @@ dequantization error bound, edge-to-code-0, and agreement with the independent C
 Attention: torch's CPU float64 scaled_dot_product_attention (sink = extra zero key with additive mask) on the
 golden cases and on random ones; invariants of the reference's split-K algebra (block size, key permutation,
 GQA == MHA with repeated K/V, single key, empty range, garbage outside [start, n)).
-Masks: chain tree == causal, the reference's branch formula == ancestor-or-self of the parent array, brute force.
+Masks: chain tree == causal, the reference's branch formula == ancestor-or-self of the parent array, brute force;
+the sliding window against a brute-force ring buffer, and banded == whole under the window mask.
 qk_norm_rope: torch RMS norm + complex RoPE in float64 within the reference's bar 0.02 max|ref|
 (tests/test_flint.py:235-236); v bit-exact.
 """
@@ -196,6 +197,47 @@ def test_ancestor_mask_brute_force():
                 anc.add(j)
                 j = parents[j]
             assert set(np.nonzero(m[i])[0].tolist()) == anc
+
+
+def test_window_mask_is_the_rotating_ring():
+    """The sliding-window mask against a brute-force ring of W slots (what a RotatingKVCache of max_size W holds
+    after writing positions 0..pos: the keys query pos attends to), its closed-form row counts, W >= N being the
+    causal mask, and the host mask builder (mlx-lm's create_causal_mask with window_size)."""
+    from locals_amd import qkv
+
+    for L, N, W in ((5, 12, 3), (12, 12, 1), (7, 30, 9), (16, 16, 40), (9, 9, 9)):
+        m = oa.window_mask(L, N, W)
+        for i in range(L):
+            pos = N - L + i
+            ring = [-1] * W
+            for t in range(pos + 1):
+                ring[t % W] = t
+            assert set(np.nonzero(m[i])[0].tolist()) == {t for t in ring if t >= 0}
+            assert int(m[i].sum()) == min(W, pos + 1) and m[i, pos] and not m[i, pos + 1:].any()
+        if W >= N:
+            assert np.array_equal(m, oa.causal_mask(L, N))
+        host = qkv.create_causal_mask(L, offset=N - L, window_size=W, device="cpu").numpy()
+        assert np.array_equal(host, m)
+
+
+@pytest.mark.parametrize("band", [1, 4, 7, 64])
+def test_banded_window_equals_whole_masked(band):
+    """The reference's own check (tests/test_flint.py:458-476): the chunk's attention band by band over the keys
+    each band's window reaches equals one attention over every key under the window's mask; and a window of one
+    key gives the query's own value (no sink)."""
+    g = np.random.default_rng(10)
+    B, H, KVH, L, N = 2, 4, 2, 13, 20
+    q = g.standard_normal((B, H, L, 128))
+    k = g.standard_normal((B, KVH, N, 128))
+    v = g.standard_normal((B, KVH, N, 128))
+    s = g.standard_normal(H)
+    for W in (1, 3, 9, 100):
+        whole = oa.sdpa(q, k, v, 0.09, oa.window_mask(L, N, W)[None, None], s, dtype="float64")
+        assert np.abs(oa.banded_sdpa(q, k, v, 0.09, W, s, band=band, dtype="float64") - whole).max() < 1e-12
+        ref = _sdpa64(q, k, v, 0.09, oa.window_mask(L, N, W)[None, None], s)
+        assert np.abs(whole - ref).max() < 1e-9
+    one = oa.sdpa(q, k, v, 0.09, oa.window_mask(L, N, 1)[None, None], None, dtype="float64")
+    assert np.abs(one - np.repeat(v[:, :, N - L:], H // KVH, axis=1)).max() < 1e-12
 
 
 def test_sdpa_random_masks_vs_torch():
