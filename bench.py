@@ -72,6 +72,9 @@ class Events:
 
 def config(name: str, seed: int = 0):
     g = np.random.default_rng(seed)
+    if name == "c1":
+        return dict(name="c1", workload="fp16 ragged decode: 4 rows x 2,048 keys, 16 query / 8 KV heads "
+                    "(ragged_attention, BASELINE config 1)", B=4, H=16, KVH=8, nb=np.array([2048] * 4))
     if name == "c2":
         B, H, KVH = 16, 32, 8
         nb = g.integers(1024, 32768, size=B, endpoint=True)
@@ -217,6 +220,63 @@ def bench_multi(cfg, args, dev):
     return res
 
 
+def bench_c1(cfg, args, dev):
+    """C1: attention.ragged_attention over fp16 slot-major K/V, one row a slot.  33.6 MB of K/V a step sits in the
+    256 MB MALL, so 10 buffer sets (336 MB) rotate.  Pass-1 times from its dispatch events; the step time from
+    events around the whole timed region."""
+    import torch
+
+    from locals_amd import _lib
+
+    lib = _lib.load()
+    stream = _lib.stream_of(dev)
+    R, H, KVH, n = cfg["B"], cfg["H"], cfg["KVH"], int(cfg["nb"][0])
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(99)
+    nsets = max(args.sets, 10)
+    sets = [(torch.randn((R, H, 128), generator=gen, device=dev, dtype=torch.float16),
+             torch.randn((R, KVH, n, 128), generator=gen, device=dev, dtype=torch.float16),
+             torch.randn((R, KVH, n, 128), generator=gen, device=dev, dtype=torch.float16)) for _ in range(nsets)]
+    slots = torch.arange(R, dtype=torch.int32, device=dev)
+    nkeys = torch.full((R,), n, dtype=torch.int32, device=dev)
+    blk = args.block or 0
+    nbytes = int(lib.lcl_decode_workspace_bytes(R, H, n, blk))
+    ws = torch.empty(nbytes // 4 + 1, dtype=torch.float32, device=dev)
+    out = torch.empty((R, H, 128), dtype=torch.float16, device=dev)
+    P_ = _lib.ptr
+    ev = Events(2 * args.steps + 2)
+
+    def run(i, e0=None, e1=None):
+        q, K, V = sets[i % nsets]
+        rc = lib.lcl_ragged_attention_ex(P_(q), 0, P_(K), P_(V), 0, P_(slots), P_(nkeys), float(1 / np.sqrt(128)),
+                                         None, R, H, R, KVH, 128, n, blk, P_(out), P_(ws), nbytes, stream, e0, e1)
+        _lib.check(rc, "lcl_ragged_attention_ex")
+
+    for i in range(args.warmup):
+        run(i)
+    torch.cuda.synchronize()
+    hip = ev.hip
+    hip.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+    hip.hipEventRecord(ev.ev[-2], stream)
+    every = max(1, args.p1_every)
+    for i in range(args.steps):
+        if i % every == 0:
+            run(i, ev.ev[2 * i], ev.ev[2 * i + 1])
+        else:
+            run(i)
+    hip.hipEventRecord(ev.ev[-1], stream)
+    torch.cuda.synchronize()
+    step_us = ev.ms(2 * args.steps, 2 * args.steps + 1) * 1e3 / args.steps
+    p1 = np.array([ev.ms(2 * i, 2 * i + 1) for i in range(0, args.steps, every)]) * 1e3
+    ev.close()
+    kv = R * KVH * n * 512
+    b_step = kv + 2 * R * H * 128 * 2
+    return {"kernel": "ragged_pass1_16", "us_per_step": round(step_us, 2), "GBs_step": round(b_step / step_us / 1e3, 1),
+            "hbm_frac_step": round(b_step / step_us / 1e3 / HBM_PEAK_GBS, 4), "pass1_avg_us": round(float(p1.mean()), 2),
+            "pass1_GBs": round((kv + R * H * 256) / float(p1.mean()) / 1e3, 1), "bytes_per_step": b_step,
+            "buffer_sets": nsets}
+
+
 def build_sets(cfg, nsets, dev):
     import torch
 
@@ -333,6 +393,9 @@ def main():
     cfg = config(args.config)
     if args.block is not None:
         qkv.BLOCK = args.block
+    if cfg["name"] == "c1":
+        print(json.dumps({"config": cfg["workload"], "ragged_decode": bench_c1(cfg, args, dev)}), flush=True)
+        return
     if cfg["name"] in ("c4", "c5", "w1"):
         from locals_amd import sdpa
 

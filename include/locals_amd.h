@@ -67,6 +67,13 @@ int lcl_ragged_attention(const void* q, int qdt, const void* keys, const void* v
                          const int32_t* nkeys, float scale, const float* scale_dev, int R, int H, int n_slots, int Hkv, int head_dim, int cap,
                          int block, void* out, void* workspace, size_t workspace_bytes, void* stream);
 
+/* Profiling form of lcl_ragged_attention: pass 1's dispatch bracketed by two
+ * hipEvent_t.  No counterpart in the reference. */
+int lcl_ragged_attention_ex(const void* q, int qdt, const void* keys, const void* values, int kvdt,
+                            const int32_t* slots, const int32_t* nkeys, float scale, const float* scale_dev, int R,
+                            int H, int n_slots, int Hkv, int head_dim, int cap, int block, void* out, void* workspace,
+                            size_t workspace_bytes, void* stream, void* ev_start, void* ev_stop);
+
 /* BatchQuantizedKVCache.update_and_fetch's store (locals/qkv.py:309-326): MLX
  * affine 8-bit quantization (mx.quantize, group 64, bits 8, called at
  * locals/qkv.py:322-323) of a step's new keys k and values v, each

@@ -31,6 +31,7 @@ SIGNATURES = {
     "lcl_qkv_attend": (I, [P, I, P, P, P, P, P, P, I, P, P, F, I, I, I, I, I, I, I, P, P, Z, P]),
     "lcl_qkv_attend_ex": (I, [P, I, P, P, P, P, P, P, I, P, P, F, I, I, I, I, I, I, I, P, P, Z, P, P, P]),
     "lcl_ragged_attention": (I, [P, I, P, P, I, P, P, F, P, I, I, I, I, I, I, I, P, P, Z, P]),
+    "lcl_ragged_attention_ex": (I, [P, I, P, P, I, P, P, F, P, I, I, I, I, I, I, I, P, P, Z, P, P, P]),
     "lcl_quantize_append": (I, [P, P, I, P, P, P, P, P, P, I, I, I, I, I, I, I, P]),
     "lcl_dequantize": (I, [P, P, P, I, ctypes.c_longlong, I, P, I, P]),
     "lcl_sdpa_workspace_bytes": (Z, [I, I, I, I, I]),

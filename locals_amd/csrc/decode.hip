@@ -1278,7 +1278,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
 }
 
 // ------------------------------------------------------------------- pass 2
-// Grid (row x head, S slices of 128 / S dims), S = 1..32 chosen so the grid is ~2048
+// Grid (row x head, S slices of 128 / S dims), S = 1..32 chosen so the grid is ~1024
 // workgroups; a workgroup is 8 S part lanes x 32 / S dim lanes (4 dims each).  Part lane c
 // merges parts c, c + 8 S, ... online (running max, rescaled sums).  The
 // first part's loads do not wait for the part count: they go out with the row-length reads
@@ -1355,7 +1355,7 @@ __global__ __launch_bounds__(256) void decode_combine(CombineParams p) {
     o2.w = __shfl_xor(acc.w, x);
     lse_merge(m, L, acc, m2, l2, o2);
   }
-  __shared__ float4 s_o[4][8];
+  __shared__ float4 s_o[4][32];  // a wave's merged dim lanes (nd = 32 / S of them)
   __shared__ float s_m[4], s_l[4];
   if (lane < nd) {
     s_o[wave][lane] = acc;
@@ -1432,22 +1432,36 @@ static void launch_q8(int qdt, int sdt, dim3 grid, hipStream_t stream, hipEvent_
   }
 }
 
-static void launch_16(int qdt, int kvdt, dim3 grid, hipStream_t stream, const DecodeParams& p) {
+template <int QDT, int KVDT>
+static void launch_16_t(dim3 grid, hipStream_t stream, hipEvent_t e0, hipEvent_t e1, const DecodeParams& p) {
+  hipExtLaunchKernelGGL((ragged_pass1_16<QDT, KVDT>), grid, dim3(256), 0, stream, e0, e1, 0, p);
+}
+
+static void launch_16(int qdt, int kvdt, dim3 grid, hipStream_t stream, hipEvent_t e0, hipEvent_t e1,
+                      const DecodeParams& p) {
   if (kvdt == DT_BF16) {
-    if (qdt == DT_F16) hipLaunchKernelGGL((ragged_pass1_16<DT_F16, DT_BF16>), grid, dim3(256), 0, stream, p);
-    else if (qdt == DT_BF16) hipLaunchKernelGGL((ragged_pass1_16<DT_BF16, DT_BF16>), grid, dim3(256), 0, stream, p);
-    else hipLaunchKernelGGL((ragged_pass1_16<DT_F32, DT_BF16>), grid, dim3(256), 0, stream, p);
+    if (qdt == DT_F16) launch_16_t<DT_F16, DT_BF16>(grid, stream, e0, e1, p);
+    else if (qdt == DT_BF16) launch_16_t<DT_BF16, DT_BF16>(grid, stream, e0, e1, p);
+    else launch_16_t<DT_F32, DT_BF16>(grid, stream, e0, e1, p);
   } else {
-    if (qdt == DT_F16) hipLaunchKernelGGL((ragged_pass1_16<DT_F16, DT_F16>), grid, dim3(256), 0, stream, p);
-    else if (qdt == DT_BF16) hipLaunchKernelGGL((ragged_pass1_16<DT_BF16, DT_F16>), grid, dim3(256), 0, stream, p);
-    else hipLaunchKernelGGL((ragged_pass1_16<DT_F32, DT_F16>), grid, dim3(256), 0, stream, p);
+    if (qdt == DT_F16) launch_16_t<DT_F16, DT_F16>(grid, stream, e0, e1, p);
+    else if (qdt == DT_BF16) launch_16_t<DT_BF16, DT_F16>(grid, stream, e0, e1, p);
+    else launch_16_t<DT_F32, DT_F16>(grid, stream, e0, e1, p);
   }
 }
 
-// pass 2 dim slices: the largest power of two in [4, 32] keeping the grid within ~2048 workgroups
+// pass 2 dim slices: the largest power of two in [1, 32] keeping the grid within ~1024 workgroups (C2's 512
+// row-heads take 2, C3's 16 take 32)
 static int comb_slices(int rows_heads) {
-  int S = 4;
-  while (S < kCombMaxSlices && (long long)rows_heads * S * 2 <= 2048) S <<= 1;
+  static int forced = -1;
+  if (forced < 0) {  // LOCALS_AMD_COMB_SLICES forces the slice count (a power of two in [1, 32]; tuning)
+    const char* e = getenv("LOCALS_AMD_COMB_SLICES");
+    const int v = e ? atoi(e) : 0;
+    forced = (v >= 1 && v <= kCombMaxSlices && (v & (v - 1)) == 0) ? v : 0;
+  }
+  if (forced) return forced;
+  int S = 1;
+  while (S < kCombMaxSlices && (long long)rows_heads * S * 2 <= 1024) S <<= 1;
   return S;
 }
 
@@ -1551,6 +1565,14 @@ int lcl_qkv_attend_ex(const void* q, int qdt, const uint32_t* kw, const void* ks
 int lcl_ragged_attention(const void* q, int qdt, const void* keys, const void* values, int kvdt, const int32_t* slots,
                          const int32_t* nkeys, float scale, const float* scale_dev, int R, int H, int n_slots, int Hkv, int hd, int cap,
                          int block, void* out, void* workspace, size_t workspace_bytes, void* stream_) {
+  return lcl_ragged_attention_ex(q, qdt, keys, values, kvdt, slots, nkeys, scale, scale_dev, R, H, n_slots, Hkv, hd,
+                                 cap, block, out, workspace, workspace_bytes, stream_, nullptr, nullptr);
+}
+
+int lcl_ragged_attention_ex(const void* q, int qdt, const void* keys, const void* values, int kvdt,
+                            const int32_t* slots, const int32_t* nkeys, float scale, const float* scale_dev, int R,
+                            int H, int n_slots, int Hkv, int hd, int cap, int block, void* out, void* workspace,
+                            size_t workspace_bytes, void* stream_, void* ev_start, void* ev_stop) {
   hipStream_t stream = static_cast<hipStream_t>(stream_);
   if (!q || !keys || !values || !slots || !nkeys || !out) return -1;
   if (hd != kHD) return -2;
@@ -1575,7 +1597,7 @@ int lcl_ragged_attention(const void* q, int qdt, const void* keys, const void* v
   p.scale_dev = scale_dev;
   p.qdt = qdt; p.sdt = kvdt;
   const dim3 grid(nchunks, Hkv * p.nslices, R);
-  launch_16(qdt, kvdt, grid, stream, p);
+  launch_16(qdt, kvdt, grid, stream, static_cast<hipEvent_t>(ev_start), static_cast<hipEvent_t>(ev_stop), p);
   CombineParams c{};
   c.pm = p.pm; c.pl = p.pl; c.po = p.po; c.sinks = nullptr; c.out = out;
   c.start = nullptr; c.nkeys = nkeys; c.n = cap; c.cap = cap; c.H = H; c.nchunks = nchunks; c.chunk = chunk;

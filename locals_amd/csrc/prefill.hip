@@ -599,31 +599,44 @@ struct SdpaCombineParams {
   int rows, H, L, nchunks, odt;
 };
 
+// One online pass over the chunks (running max, rescaled sums), their loads issued ahead of the merges; a half
+// wave a row, 4 dims a lane.  Chunks with m = -inf (no key; their o was not written) weigh 0.
 __global__ __launch_bounds__(256) void sdpa_combine(SdpaCombineParams p) {
-  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 8 + (threadIdx.x >> 5);
+  const int lane = threadIdx.x & 31;
   if (row >= p.rows) return;
   const int head = (row / p.L) % p.H;
   const size_t base = size_t(row) * p.nchunks;
-  const float sink = p.sinks ? p.sinks[head] * kLog2e : -INFINITY;
-  float M = sink;
-  for (int c = 0; c < p.nchunks; c++) M = fmaxf(M, p.pm[base + c]);
-  float L = 0.0f, o0 = 0.0f, o1 = 0.0f;
-  if (M != -INFINITY) {
-    L = sink == -INFINITY ? 0.0f : fast_exp2(sink - M);
-    for (int c = 0; c < p.nchunks; c++) {
-      const float mc = p.pm[base + c];
-      if (!(mc > -INFINITY)) continue;
-      const float w = fast_exp2(mc - M);
-      L += w * p.pl[base + c];
-      const float2 o = reinterpret_cast<const float2*>(p.po + (base + c) * kD)[lane];
-      o0 += w * o.x;
-      o1 += w * o.y;
-    }
+  const float4* po4 = reinterpret_cast<const float4*>(p.po) + base * (kD / 4) + lane;
+  float m = -INFINITY, L = 0.0f;
+  float4 o = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll 8
+  for (int c = 0; c < p.nchunks; c++) {
+    const float mc = p.pm[base + c], lc = p.pl[base + c];
+    const float4 oc = po4[size_t(c) * (kD / 4)];
+    if (!(mc > -INFINITY)) continue;
+    const float mn = fmaxf(m, mc);
+    const float a = m == -INFINITY ? 0.0f : fast_exp2(m - mn), w = fast_exp2(mc - mn);
+    o.x = o.x * a + oc.x * w;
+    o.y = o.y * a + oc.y * w;
+    o.z = o.z * a + oc.z * w;
+    o.w = o.w * a + oc.w * w;
+    L = L * a + lc * w;
+    m = mn;
   }
-  const float inv = L > 0.0f ? 1.0f / L : 0.0f;
-  store_from_f32(p.out, size_t(row) * kD + 2 * lane, o0 * inv, p.odt);
-  store_from_f32(p.out, size_t(row) * kD + 2 * lane + 1, o1 * inv, p.odt);
+  const float sink = p.sinks ? p.sinks[head] * kLog2e : -INFINITY;
+  const float M = fmaxf(m, sink);
+  float f = 0.0f, Lt = 0.0f;
+  if (M != -INFINITY) {
+    f = m == -INFINITY ? 0.0f : fast_exp2(m - M);
+    Lt = f * L + (sink == -INFINITY ? 0.0f : fast_exp2(sink - M));
+  }
+  const float w = Lt > 0.0f ? f / Lt : 0.0f;
+  const size_t ob = size_t(row) * kD + 4 * lane;
+  store_from_f32(p.out, ob + 0, o.x * w, p.odt);
+  store_from_f32(p.out, ob + 1, o.y * w, p.odt);
+  store_from_f32(p.out, ob + 2, o.z * w, p.odt);
+  store_from_f32(p.out, ob + 3, o.w * w, p.odt);
 }
 
 template <int QDT, int SDT, int FMT, int MT, int MASK>
@@ -752,7 +765,7 @@ int lcl_sdpa_ex(const void* q, int qdt, int kvfmt, const uint32_t* kw, const voi
   }
   if (!p.direct) {
     SdpaCombineParams c{p.pm, p.pl, p.po, sinks, out, B * H * L, H, L, nchunks, qdt};
-    hipLaunchKernelGGL(sdpa_combine, dim3((B * H * L + 3) / 4), dim3(256), 0, stream, c);
+    hipLaunchKernelGGL(sdpa_combine, dim3((B * H * L + 7) / 8), dim3(256), 0, stream, c);
   }
   return int(hipGetLastError());
 }
