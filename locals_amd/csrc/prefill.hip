@@ -20,10 +20,10 @@
 // as the reference's dequantized() feeds its attention in T) -- K row-major and V
 // transposed, rows padded so the operand reads are bank-conflict free -- and every wave
 // reuses the tile for its 16 rows:
-//  * S^T = K Q^T on v_mfma_f32_16x16x16 (A = 16 keys x 16 dims from LDS, B = Q^T from
+//  * S^T = K Q^T on v_mfma_f32_16x16x32 (A = 16 keys x 32 dims from LDS, B = Q^T from
 //    registers): lane l gets S[row l % 16][keys 4 (l / 16) + i] -- the softmax state of
 //    a row lives in one lane column, its max needs two cross-lane steps;
-//  * O^T = V^T P^T (A = V^T 16 dims x 16 keys from LDS, B = P^T in the S^T registers):
+//  * O^T = V^T P^T (A = V^T 16 dims x 32 keys from LDS, B = P^T in the S^T registers):
 //    lane l holds O[row l % 16][dims 4 (l / 16) + i], so rescaling O is lane-local.
 //  P is rounded to the MFMA type, as MLX's attention does; accumulation is fp32.
 //  A partial (m, l, o[128]) per (row, chunk) goes to the workspace; sdpa_combine joins
@@ -409,19 +409,36 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   // Each K / V^T operand fragment is read from LDS once and applied to every row tile of the wave, so a
   // fragment is live for RT MFMAs only (the row tiles' scores, P and O are what stays in registers).
   auto compute = [&](int t0, int buf) __attribute__((always_inline)) {
-    // S^T = K Q^T: st[r][t][i] = S[row][t0 + 16 t + 4 q4 + i]
+    // S^T = K Q^T: st[r][t][i] = S[row][t0 + 16 t + 4 q4 + i].  Where registers allow (causal and window masks,
+    // one row tile), the 32-dim step kk is the outer loop, so the 4 RT accumulators are independent chains and a
+    // step's four K fragments are read together; otherwise a key block t at a time.
+    constexpr bool kStepOuter = MASK == MK_CAUSAL || MASK == MK_WINDOW || RT == 1;
     f4 st[RT][4];
 #pragma unroll
-    for (int t = 0; t < 4; t++) {
+    for (int t = 0; t < 4; t++)
 #pragma unroll
       for (int r = 0; r < RT; r++) st[r][t] = f4{0.0f, 0.0f, 0.0f, 0.0f};
-      const uint16_t* krow = &Ks[buf][(16 * t + c16) * kKsStride + 8 * q4];
+    const uint16_t* kbase = &Ks[buf][c16 * kKsStride + 8 * q4];
+    if constexpr (kStepOuter) {
 #pragma unroll
       for (int kk = 0; kk < 4; kk++) {
-        const uint4 kf = *reinterpret_cast<const uint4*>(krow + 32 * kk);
+        uint4 kf[4];
 #pragma unroll
-        for (int r = 0; r < RT; r++) st[r][t] = mma32<MT>(kf, qb[r][kk], st[r][t]);
+        for (int t = 0; t < 4; t++) kf[t] = *reinterpret_cast<const uint4*>(kbase + 16 * t * kKsStride + 32 * kk);
+#pragma unroll
+        for (int t = 0; t < 4; t++)
+#pragma unroll
+          for (int r = 0; r < RT; r++) st[r][t] = mma32<MT>(kf[t], qb[r][kk], st[r][t]);
       }
+    } else {
+#pragma unroll
+      for (int t = 0; t < 4; t++)
+#pragma unroll
+        for (int kk = 0; kk < 4; kk++) {
+          const uint4 kf = *reinterpret_cast<const uint4*>(kbase + 16 * t * kKsStride + 32 * kk);
+#pragma unroll
+          for (int r = 0; r < RT; r++) st[r][t] = mma32<MT>(kf, qb[r][kk], st[r][t]);
+        }
     }
     // a tile every key of which every row of the wave sees needs no mask (for causal prefill, all but the
     // diagonal tiles); rows past the row count are not written, so they need none either
@@ -511,11 +528,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     constexpr int kWaitOne = (0xF << 8) | (0x7 << 4) | 5;
     constexpr int kWaitAll = (0xF << 8) | (0x7 << 4);
     constexpr int kWaitLds = (0x3 << 14) | (0x7 << 4) | 0xF;
-    // a workgroup barrier that leaves the other slot's loads in flight (__syncthreads would wait for them)
+    // a workgroup barrier for LDS that leaves the other slot's loads in flight (__syncthreads would wait for them)
     auto barrier = [&]() __attribute__((always_inline)) {
       __builtin_amdgcn_s_waitcnt(kWaitLds);
       __builtin_amdgcn_s_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
     };
     auto step = [&](int t0, uint8_t* S) __attribute__((always_inline)) {
       if (t0 + kKT < khi) __builtin_amdgcn_s_waitcnt(kWaitOne);
