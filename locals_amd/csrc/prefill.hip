@@ -275,10 +275,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   };
 
   // dequantize (8-bit) or copy (16-bit) a staged tile into LDS buffer `buf`; keys outside [klo, khi) become 0
-  auto stage = [&](int t0, const RawTile& T, int buf) __attribute__((always_inline)) {
+  // (MASKED: the tile straddles an end of the range; otherwise every key is inside and no test is made)
+  auto stage = [&](int t0, const RawTile& T, int buf, auto masked) __attribute__((always_inline)) {
+    constexpr bool MASKED = decltype(masked)::value;
     {
       const int kg = t0 + kkey;
-      const bool kin = kg >= klo && kg < khi;
+      const bool kin = !MASKED || (kg >= klo && kg < khi);
       uint32_t o[16];
       if constexpr (FMT == KV_Q8) {
         const uint32_t cw[8] = {T.k[0].x, T.k[0].y, T.k[0].z, T.k[0].w, T.k[1].x, T.k[1].y, T.k[1].z, T.k[1].w};
@@ -315,7 +317,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
       for (int k = 0; k < 4; k++) {
         const int kg = t0 + 4 * vkq + k;
-        vin[k] = kg >= klo && kg < khi;
+        vin[k] = !MASKED || (kg >= klo && kg < khi);
       }
       uint32_t pr[8][2];  // dims 8 vdq + e: (keys 0,1), (keys 2,3)
       if constexpr (FMT == KV_Q8) {
@@ -409,10 +411,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   // Each K / V^T operand fragment is read from LDS once and applied to every row tile of the wave, so a
   // fragment is live for RT MFMAs only (the row tiles' scores, P and O are what stays in registers).
   auto compute = [&](int t0, int buf) __attribute__((always_inline)) {
-    // S^T = K Q^T: st[r][t][i] = S[row][t0 + 16 t + 4 q4 + i].  Where registers allow (causal and window masks,
-    // one row tile), the 32-dim step kk is the outer loop, so the 4 RT accumulators are independent chains and a
-    // step's four K fragments are read together; otherwise a key block t at a time.
-    constexpr bool kStepOuter = MASK == MK_CAUSAL || MASK == MK_WINDOW || RT == 1;
+    // S^T = K Q^T: st[r][t][i] = S[row][t0 + 16 t + 4 q4 + i].  Where registers allow (causal mask, one row
+    // tile), the 32-dim step kk is the outer loop, so the 4 RT accumulators are independent chains and a step's
+    // four K fragments are read together; otherwise a key block t at a time.
+    constexpr bool kStepOuter = MASK == MK_CAUSAL || RT == 1;
     f4 st[RT][4];
 #pragma unroll
     for (int t = 0; t < 4; t++)
@@ -540,7 +542,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       barrier();  // the slot's tile is in LDS; every wave is done with the previous tile's operands
       RawTile T;
       load_lds(S, T);
-      stage(t0, T, 0);
+      if (t0 >= klo && t0 + kKT <= khi) stage(t0, T, 0, std::false_type{});
+      else stage(t0, T, 0, std::true_type{});
       barrier();  // operands ready; the slot is free
       if (t0 + 2 * kKT < khi) dma(t0 + 2 * kKT, S);
       compute(t0, 0);
@@ -558,14 +561,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   } else {
     RawTile A, B;
     load(tfirst, A);
-    stage(tfirst, A, 0);
+    stage(tfirst, A, 0, std::true_type{});
     __syncthreads();
     int buf = 0;
     for (int t0 = tfirst; t0 < khi; t0 += kKT) {
       const bool more = t0 + kKT < khi;
       if (more) load(t0 + kKT, B);
       compute(t0, buf);
-      if (more) stage(t0 + kKT, B, buf ^ 1);
+      if (more) {
+        if (t0 + kKT >= klo && t0 + 2 * kKT <= khi) stage(t0 + kKT, B, buf ^ 1, std::false_type{});
+        else stage(t0 + kKT, B, buf ^ 1, std::true_type{});
+      }
       __syncthreads();
       buf ^= 1;
     }
@@ -658,9 +664,9 @@ __global__ __launch_bounds__(256) void sdpa_combine(SdpaCombineParams p) {
 
 template <int QDT, int SDT, int FMT, int MT, int MASK>
 static void launch_rt(int rt, dim3 grid, hipStream_t s, hipEvent_t e0, hipEvent_t e1, const SdpaParams& p) {
-  // two row tiles only for 8-bit keys and values under masks read per key pair or none (a dense mask's byte loads
-  // for two tiles would not fit in registers)
-  if constexpr (FMT == KV_Q8 && MASK != MK_DENSE) {
+  // two row tiles only for 8-bit keys and values without a dense or window mask (their per-key tests for two
+  // tiles would not fit in registers)
+  if constexpr (FMT == KV_Q8 && MASK != MK_DENSE && MASK != MK_WINDOW) {
     if (rt == 2) {
       hipExtLaunchKernelGGL((sdpa_pass1<QDT, SDT, FMT, MT, MASK, 2>), grid, dim3(256), 0, s, e0, e1, 0, p);
       return;
@@ -744,10 +750,10 @@ int lcl_sdpa_ex(const void* q, int qdt, int kvfmt, const uint32_t* kw, const voi
   if (mask_kind == MK_TREE && (!tree || L > 64 || L > N)) return -2;
   if (mask_kind == MK_DENSE && !dense) return -1;
   // row tiles a wave: two (128 rows a workgroup) for 8-bit keys and values when there are more than 64 rows,
-  // halving the dequantization and the operand reads per row; one otherwise (16-bit needs no dequantization; a
-  // dense mask's per-row byte reads would not fit beside two tiles' registers)
+  // halving the dequantization and the operand reads per row; one otherwise (16-bit needs no dequantization; the
+  // dense and window masks' per-key tests would not fit beside two tiles' registers)
   const int rows = L * (H / KVH);
-  const int rt = (kvfmt == KV_Q8 && mask_kind != MK_DENSE && rows > 64) ? 2 : 1;
+  const int rt = (kvfmt == KV_Q8 && mask_kind != MK_DENSE && mask_kind != MK_WINDOW && rows > 64) ? 2 : 1;
   int chunk = sdpa_chunk(block, B, H, L, N, 64 * rt);
   int nchunks = N > 0 ? (N + chunk - 1) / chunk : 1;
   if (mask_kind == MK_WINDOW && N > 0) {
