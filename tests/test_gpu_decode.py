@@ -154,3 +154,59 @@ def test_ragged_matches_oracle(dev, H, Hkv, kvdt):
     tol = 2e-3 if kvdt == "float16" else 2 ** -7 * (1 + np.abs(ref).max())
     assert np.abs(_out(got) - ref).max() <= tol
     assert (_out(got)[2] == 0).all()
+
+
+def test_attend_many_rows(dev):
+    """More than 64 rows (the quad pass 1 then scans the rows 64 at a time to split its work) with ragged left
+    padding, empty rows and a row whose keys start mid-tile."""
+    from locals_amd import qkv
+
+    g = rng(14)
+    B, H, KVH, cap, n = 100, 8, 2, 640, 600
+    q = normal16(g, (B, H, 1, 128))
+    K, V = q8_cache(g, B, KVH, cap, kscale=2.0)
+    sinks = normal16(g, (H,), 2.0)
+    start = g.integers(0, n + 1, size=B).astype(np.int32)
+    start[[3, 40, 77]] = n  # empty rows
+    start[[5, 90]] = 0
+    got = qkv.attend(to_torch(q, dev), triple_to_torch(K, dev), triple_to_torch(V, dev), n, to_torch(sinks, dev),
+                     0.0884, to_torch(start, dev))
+    torch.cuda.synchronize()
+    ref = oattn.attend(q, K, V, n, sinks, 0.0884, start)
+    assert np.abs(_out(got) - ref).max() <= 2e-3
+    assert not _out(got)[[3, 40, 77]].any()
+
+
+def test_attend_c2_full_size_vs_c_restatement(dev):
+    """BASELINE config 2 at its full size (16 rows, contexts U[1024, 32768] seeded as bench.py draws them, 32/8
+    heads, 8-bit K/V made by the quantize kernel on the GPU) against the C restatement of the reference's two
+    passes (oracle/c, fp32, the reference's block sizes), with sinks."""
+    import bench
+    from locals_amd import qkv
+    from oracle import cbind
+
+    cfg = bench.config("c2")
+    B, H, KVH, nb = cfg["B"], cfg["H"], cfg["KVH"], cfg["nb"]
+    n = int(nb.max())
+    cap = (n + 255) // 256 * 256
+    print(f"c2 full size: sum n_b = {int(nb.sum())}, cap = {cap}", flush=True)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(77)
+    K = qkv._zeros(B, KVH, cap, 128, torch.float16, dev)
+    V = qkv._zeros(B, KVH, cap, 128, torch.float16, dev)
+    for b in range(B):
+        kf = torch.randn((1, KVH, cap, 128), generator=gen, device=dev, dtype=torch.float16)
+        vf = torch.randn((1, KVH, cap, 128), generator=gen, device=dev, dtype=torch.float16)
+        qkv.quantize_into(kf, vf, tuple(a[b:b + 1] for a in K), tuple(a[b:b + 1] for a in V), 0)
+    q = torch.randn((B, H, 1, 128), generator=gen, device=dev, dtype=torch.float16)
+    sinks = torch.randn((H,), generator=gen, device=dev, dtype=torch.float16) * 2
+    start = torch.tensor(n - nb, dtype=torch.int32, device=dev)
+    got = qkv.attend(q, K, V, n, sinks, 1 / np.sqrt(128), start)
+    torch.cuda.synchronize()
+    host = lambda t: t.cpu().numpy()  # noqa: E731
+    Kn = (host(K[0]).view(np.uint32), host(K[1]), host(K[2]))
+    Vn = (host(V[0]).view(np.uint32), host(V[1]), host(V[2]))
+    ref = cbind.attend_q8(host(q), Kn, Vn, n, host(sinks), 1 / np.sqrt(128), host(start), threads=16)
+    err = float(np.abs(_out(got) - ref.astype(np.float64)).max())
+    print(f"c2 full size max |gpu - C| = {err:.3g}", flush=True)
+    assert err <= 2e-3
