@@ -48,6 +48,11 @@ constexpr float kThr = 6.0f;
 // V^T row d keeps its 16 four-key slots XOR-permuted by (d >> 3) & 15: the staging writes, which take 8
 // consecutive rows a thread and rows 8 apart across a wave's lanes, then fall in distinct banks
 __device__ __forceinline__ int vt_swz(int d) { return (d >> 3) & 15; }
+// A 16-bit K + V tile (64 key rows of 256 B each).  Key row r keeps its 16-byte chunk c at slot c ^ sw16(r), a
+// permutation of r's low four bits: the K operand reads (16 rows, one chunk each) are then free of bank
+// conflicts and the transposing V reads (16 consecutive rows, two chunks each) two-way, the least for 512 B.
+constexpr int kRaw16 = 2 * kKT * kD * 2;
+__device__ __forceinline__ int sw16(int r) { return ((r << 1) & 6) | (r & 8) | ((r >> 2) & 1); }
 
 enum MaskKind { MK_NONE = 0, MK_CAUSAL = 1, MK_TREE = 2, MK_DENSE = 3, MK_WINDOW = 4 };
 enum KvFmt { KV_Q8 = 0, KV_16 = 1 };
@@ -87,10 +92,12 @@ __device__ __forceinline__ uint16_t to_mt(float x) {
   else return __builtin_bit_cast(uint16_t, _Float16(x));
 }
 
-// two floats -> a packed pair of the MFMA type, round to nearest even
+// two floats -> a packed pair of the MFMA type, round to nearest even (bf16: one v_cvt_pk_bf16_f32)
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 template <int MT>
 __device__ __forceinline__ uint32_t pack2(float a, float b) {
-  if constexpr (MT == DT_BF16) return uint32_t(f32_to_bf16_bits(a)) | (uint32_t(f32_to_bf16_bits(b)) << 16);
+  if constexpr (MT == DT_BF16) return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, bf16x2));
   else return __builtin_bit_cast(uint32_t, h2{_Float16(a), _Float16(b)});
 }
 
@@ -124,13 +131,46 @@ struct RawTile {
   uint32_t vs[4], vb[4];
 };
 
+// Direct buffer -> LDS loads issued as asm, outside the compiler's LDS-DMA wait tracking (merged at a loop head it
+// cannot tell two slots apart and makes every read of one wait for the loads into the other).  Their completion
+// is awaited with explicit s_waitcnt vmcnt by the caller, before a barrier.  Lane l's 16 bytes at voff land at
+// lds + 16 l; the descriptor covers `bytes` bytes (loads past it read 0), raw, non-temporal.
+typedef uint32_t sg4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ sg4 rsrc_words(const void* p, uint32_t bytes) {
+  const uint64_t a = reinterpret_cast<uint64_t>(p);
+  return sg4{uint32_t(a), uint32_t(a >> 32) & 0xffffu, bytes, 0x00020000u};
+}
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return uint32_t(uintptr_t((const __attribute__((address_space(3))) uint8_t*)(p)));
+}
+__device__ __forceinline__ void dma16(sg4 r, uint32_t lds, uint32_t voff) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen nt lds" : : "s"(lds), "v"(voff), "s"(r)
+               : "memory", "m0");
+}
+
+// ds_read_b64_tr_b16: in each 16-lane group, lane i's element e is element i % 4 of the 8 bytes that lane
+// 4 e + i / 4 of the group addresses (checked in bounds on the MI355X).
+typedef short s4v __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint2 lds_read_tr16(const uint8_t* p) {
+  const s4v v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s4v*)(p));
+  return __builtin_bit_cast(uint2, v);
+}
+
 // One workgroup: RT x 64 rows of (batch row b, kv head kvh) -- a row is one (query, head) -- and the keys of
-// chunk c.  Per 64-key tile: the next tile's raw bytes are loaded into registers while this tile's MFMAs run,
-// then dequantized into the other LDS buffer (double-buffered, one barrier a tile).
+// chunk c.  8-bit: per 64-key tile the raw bytes arrive in one of two LDS slots while the other's tile is
+// dequantized into the operand buffer and multiplied.  16-bit: the K and V tiles arrive in one of two slots and
+// are multiplied in place while the next tile's loads are in flight.
 template <int QDT, int SDT, int FMT, int MT, int MASK, int RT>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void sdpa_pass1(SdpaParams p) {
-  const int c = blockIdx.x, rb = blockIdx.y;
-  const int b = blockIdx.z / p.KVH, kvh = blockIdx.z % p.KVH;
+  // XCD-aware order: the hardware deals workgroups to the 8 XCDs round-robin, so physical workgroup P runs on
+  // XCD P % 8; logical workgroup (P % 8) * ceil(total / 8) + P / 8 gives each XCD a contiguous run of (chunk,
+  // row block, batch row x kv head) -- the same kv head's K/V for all of it, which its own L2 then holds
+  const int total = p.nchunks * p.nrowblocks * p.B * p.KVH;
+  const int lg = int(blockIdx.x % 8u) * ((total + 7) / 8) + int(blockIdx.x / 8u);
+  if (lg >= total) return;  // padding of the grid to a multiple of 8
+  const int c = lg % p.nchunks, rb = (lg / p.nchunks) % p.nrowblocks;
+  const int bz = lg / (p.nchunks * p.nrowblocks);
+  const int b = bz / p.KVH, kvh = bz % p.KVH;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63, tid = threadIdx.x;
   const int c16 = lane & 15, q4 = lane >> 4;
   const int R = p.L * p.G;
@@ -177,12 +217,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   }
 
   // 8-bit: raw tiles arrive by direct buffer->LDS loads into two named slots (one in flight while the other is
-  // staged) and are dequantized into a single operand buffer; 16-bit: register prefetch, two operand buffers
-  constexpr int NB = FMT == KV_Q8 ? 1 : 2;
-  __shared__ __attribute__((aligned(16))) uint16_t Ks[NB][kKT * kKsStride];
-  __shared__ __attribute__((aligned(16))) uint16_t Vt[NB][kD * kVtStride];
-  __shared__ __attribute__((aligned(16))) uint8_t raw0[FMT == KV_Q8 ? kRawSlot : 16];
-  __shared__ __attribute__((aligned(16))) uint8_t raw1[FMT == KV_Q8 ? kRawSlot : 16];
+  // staged) and are dequantized into one operand buffer (Ks, Vt).  16-bit: the K and V tiles arrive the same way
+  // (chunks swizzled by sw16) and are the MFMA operands themselves -- K rows read as they are, V^T through the
+  // transposing read -- so nothing is staged.
+  __shared__ __attribute__((aligned(16))) uint16_t Ks[FMT == KV_Q8 ? kKT * kKsStride : 8];
+  __shared__ __attribute__((aligned(16))) uint16_t Vt[FMT == KV_Q8 ? kD * kVtStride : 8];
+  __shared__ __attribute__((aligned(16))) uint8_t raw0[FMT == KV_Q8 ? kRawSlot : kRaw16];
+  __shared__ __attribute__((aligned(16))) uint8_t raw1[FMT == KV_Q8 ? kRawSlot : kRaw16];
 
   // Q^T as B operands: qb[r][kk] = scale log2(e) q[row][32 kk + 8 q4 + j], scaled in fp32 before its one rounding
   // to the MFMA type, so the products come out as base-2 logits
@@ -214,38 +255,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     rkb = make_rsrc(static_cast<const uint16_t*>(p.kb) + tok0 * 2, cap * 4u);
     rvs = make_rsrc(static_cast<const uint16_t*>(p.vs) + tok0 * 2, cap * 4u);
     rvb = make_rsrc(static_cast<const uint16_t*>(p.vb) + tok0 * 2, cap * 4u);
-  } else {
-    rk = make_rsrc(static_cast<const uint16_t*>(p.kf) + tok0 * kD, cap * 256u);
-    rv = make_rsrc(static_cast<const uint16_t*>(p.vf) + tok0 * kD, cap * 256u);
   }
+  const sg4 dk16 = rsrc_words(static_cast<const uint16_t*>(FMT == KV_16 ? p.kf : p.kw) + tok0 * kD, cap * 256u);
+  const sg4 dv16 = rsrc_words(static_cast<const uint16_t*>(FMT == KV_16 ? p.vf : p.vw) + tok0 * kD, cap * 256u);
   // 8-bit DMA: the scale / bias array this wave sends (wave 0 K scales, 1 K biases, 2 V scales, 3 V biases)
   const void* sarr = FMT != KV_Q8 ? p.kf : wave == 0 ? p.ks : wave == 1 ? p.kb : wave == 2 ? p.vs : p.vb;
   const BufRsrc rsw = make_rsrc(static_cast<const uint16_t*>(sarr) + tok0 * 2, cap * 4u);
   const int kkey = tid >> 2, kpart = tid & 3;   // K staging: one key, 32 dims
   const int vkq = tid >> 4, vdq = tid & 15;     // V staging: keys 4 vkq .. +3, dims 8 vdq .. +7
-
-  auto load = [&](int t0, RawTile& T) __attribute__((always_inline)) {
-    const uint32_t kk = uint32_t(t0 + kkey);
-    if constexpr (FMT == KV_Q8) {
-      T.k[0] = buf_load_b128(rk, kk * 128u + 32u * kpart, 0);
-      T.k[1] = buf_load_b128(rk, kk * 128u + 32u * kpart, 16);
-      T.ks = buf_load_b32(rks, kk * 4u, 0);
-      T.kb = buf_load_b32(rkb, kk * 4u, 0);
-#pragma unroll
-      for (int k = 0; k < 4; k++) {
-        const uint32_t vk = uint32_t(t0 + 4 * vkq + k);
-        const uint32_t lo = buf_load_b32(rv, vk * 128u + 8u * vdq, 0), hi = buf_load_b32(rv, vk * 128u + 8u * vdq, 4);
-        T.v[k] = u4{lo, hi, 0u, 0u};
-        T.vs[k] = buf_load_b32(rvs, vk * 4u, 0);
-        T.vb[k] = buf_load_b32(rvb, vk * 4u, 0);
-      }
-    } else {
-#pragma unroll
-      for (int u = 0; u < 4; u++) T.k[u] = buf_load_b128(rk, kk * 256u + 64u * kpart, 16 * u);
-#pragma unroll
-      for (int k = 0; k < 4; k++) T.v[k] = buf_load_b128(rv, uint32_t(t0 + 4 * vkq + k) * 256u + 16u * vdq, 0);
-    }
-  };
 
   // 8-bit raw tile in LDS: K codes (key-major 128 B rows, 8 KB), V codes (8 KB), ks / kb / vs / vb words (256 B
   // each).  Wave w sends K and V rows 16 w .. 16 w + 15 (two 1 KB pieces each) and the w-th scale array.
@@ -274,9 +291,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     }
   };
 
-  // dequantize (8-bit) or copy (16-bit) a staged tile into LDS buffer `buf`; keys outside [klo, khi) become 0
+  // dequantize an 8-bit tile into the operand buffer; keys outside [klo, khi) become 0
   // (MASKED: the tile straddles an end of the range; otherwise every key is inside and no test is made)
-  auto stage = [&](int t0, const RawTile& T, int buf, auto masked) __attribute__((always_inline)) {
+  auto stage = [&](int t0, const RawTile& T, auto masked) __attribute__((always_inline)) {
     constexpr bool MASKED = decltype(masked)::value;
     {
       const int kg = t0 + kkey;
@@ -301,13 +318,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             o[2 * w + 1] = pack2<MT>(sf * float((cw[w] >> 16) & 0xffu) + bf, sf * float(cw[w] >> 24) + bf);
           }
         }
-      } else {
-#pragma unroll
-        for (int u = 0; u < 4; u++) {
-          o[4 * u] = T.k[u].x; o[4 * u + 1] = T.k[u].y; o[4 * u + 2] = T.k[u].z; o[4 * u + 3] = T.k[u].w;
-        }
       }
-      uint4* dst = reinterpret_cast<uint4*>(&Ks[buf][kkey * kKsStride + kpart * 32]);
+      uint4* dst = reinterpret_cast<uint4*>(&Ks[kkey * kKsStride + kpart * 32]);
 #pragma unroll
       for (int u = 0; u < 4; u++)
         dst[u] = kin ? make_uint4(o[4 * u], o[4 * u + 1], o[4 * u + 2], o[4 * u + 3]) : make_uint4(0u, 0u, 0u, 0u);
@@ -366,24 +378,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             pr[e][1] = pack2<MT>(v[2], v[3]);
           }
         }
-      } else {
-#pragma unroll
-        for (int e = 0; e < 8; e++) {
-          const int u = e >> 1;
-          const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
-          const uint32_t w0 = u == 0 ? T.v[0].x : u == 1 ? T.v[0].y : u == 2 ? T.v[0].z : T.v[0].w;
-          const uint32_t w1 = u == 0 ? T.v[1].x : u == 1 ? T.v[1].y : u == 2 ? T.v[1].z : T.v[1].w;
-          const uint32_t w2 = u == 0 ? T.v[2].x : u == 1 ? T.v[2].y : u == 2 ? T.v[2].z : T.v[2].w;
-          const uint32_t w3 = u == 0 ? T.v[3].x : u == 1 ? T.v[3].y : u == 2 ? T.v[3].z : T.v[3].w;
-          pr[e][0] = __builtin_amdgcn_perm(w1, w0, sel);
-          pr[e][1] = __builtin_amdgcn_perm(w3, w2, sel);
-        }
       }
       const uint32_t m01 = (vin[0] ? 0xffffu : 0u) | (vin[1] ? 0xffff0000u : 0u);
       const uint32_t m23 = (vin[2] ? 0xffffu : 0u) | (vin[3] ? 0xffff0000u : 0u);
 #pragma unroll
       for (int e = 0; e < 8; e++)
-        *reinterpret_cast<uint2*>(&Vt[buf][(8 * vdq + e) * kVtStride + 4 * (vkq ^ vt_swz(8 * vdq + e))]) =
+        *reinterpret_cast<uint2*>(&Vt[(8 * vdq + e) * kVtStride + 4 * (vkq ^ vt_swz(8 * vdq + e))]) =
             make_uint2(pr[e][0] & m01, pr[e][1] & m23);
     }
   };
@@ -408,9 +408,36 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     if constexpr (MASK == MK_DENSE) drow[r] = p.dense + b * p.msb + head[r] * p.msh + qi[r] * p.msq;
   }
 
+  // The MFMA operand fragments of a tile.  8-bit: from the dequantized buffers.  16-bit: from the tile slot S --
+  // K: key 16 t + c16, dims 32 kk + 8 q4 .. +7 (one 16-byte chunk); V^T: lane (g = q4, m = c16) points the
+  // transposing read at key 32 u + 4 g + m / 4 (and + 16 for the second half), dims 16 dd + 4 (m % 4) .. +3, so
+  // its 8 values are dim 16 dd + m of the keys whose P^T the B operand holds at k = 8 q4 + j.
+  const int sk16 = sw16(c16);
+  const int vkey16 = 4 * q4 + (c16 >> 2), vsw16 = sw16(vkey16);
+  const int vch16 = (c16 & 3) >> 1, voff16 = 16384 + vkey16 * 256 + 8 * (c16 & 1);
+  auto kfrag = [&](const uint8_t* S, int t, int kk) __attribute__((always_inline)) -> uint4 {
+    if constexpr (FMT == KV_Q8)
+      return *reinterpret_cast<const uint4*>(&Ks[(16 * t + c16) * kKsStride + 8 * q4 + 32 * kk]);
+    else
+      return *reinterpret_cast<const uint4*>(S + (16 * t + c16) * 256 + 16 * ((4 * kk + q4) ^ sk16));
+  };
+  auto vfrag = [&](const uint8_t* S, int u, int dd) __attribute__((always_inline)) -> uint4 {
+    if constexpr (FMT == KV_Q8) {
+      const int vr = 16 * dd + c16, sw = vt_swz(vr);
+      const uint16_t* vrow = &Vt[vr * kVtStride];
+      const uint2 lo = *reinterpret_cast<const uint2*>(vrow + 4 * ((8 * u + q4) ^ sw));
+      const uint2 hi = *reinterpret_cast<const uint2*>(vrow + 4 * ((8 * u + 4 + q4) ^ sw));
+      return make_uint4(lo.x, lo.y, hi.x, hi.y);
+    } else {
+      const uint8_t* a = S + voff16 + 32 * u * 256 + 16 * ((2 * dd + vch16) ^ vsw16);
+      const uint2 lo = lds_read_tr16(a), hi = lds_read_tr16(a + 16 * 256);
+      return make_uint4(lo.x, lo.y, hi.x, hi.y);
+    }
+  };
+
   // Each K / V^T operand fragment is read from LDS once and applied to every row tile of the wave, so a
   // fragment is live for RT MFMAs only (the row tiles' scores, P and O are what stays in registers).
-  auto compute = [&](int t0, int buf) __attribute__((always_inline)) {
+  auto compute = [&](int t0, const uint8_t* S) __attribute__((always_inline)) {
     // S^T = K Q^T: st[r][t][i] = S[row][t0 + 16 t + 4 q4 + i].  Where registers allow (causal mask, one row
     // tile), the 32-dim step kk is the outer loop, so the 4 RT accumulators are independent chains and a step's
     // four K fragments are read together; otherwise a key block t at a time.
@@ -420,13 +447,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     for (int t = 0; t < 4; t++)
 #pragma unroll
       for (int r = 0; r < RT; r++) st[r][t] = f4{0.0f, 0.0f, 0.0f, 0.0f};
-    const uint16_t* kbase = &Ks[buf][c16 * kKsStride + 8 * q4];
     if constexpr (kStepOuter) {
 #pragma unroll
       for (int kk = 0; kk < 4; kk++) {
         uint4 kf[4];
 #pragma unroll
-        for (int t = 0; t < 4; t++) kf[t] = *reinterpret_cast<const uint4*>(kbase + 16 * t * kKsStride + 32 * kk);
+        for (int t = 0; t < 4; t++) kf[t] = kfrag(S, t, kk);
 #pragma unroll
         for (int t = 0; t < 4; t++)
 #pragma unroll
@@ -437,7 +463,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       for (int t = 0; t < 4; t++)
 #pragma unroll
         for (int kk = 0; kk < 4; kk++) {
-          const uint4 kf = *reinterpret_cast<const uint4*>(kbase + 16 * t * kKsStride + 32 * kk);
+          const uint4 kf = kfrag(S, t, kk);
 #pragma unroll
           for (int r = 0; r < RT; r++) st[r][t] = mma32<MT>(kf, qb[r][kk], st[r][t]);
         }
@@ -513,11 +539,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     for (int u = 0; u < 2; u++) {
 #pragma unroll
       for (int dd = 0; dd < 8; dd++) {
-        const int vr = 16 * dd + c16, sw = vt_swz(vr);
-        const uint16_t* vrow = &Vt[buf][vr * kVtStride];
-        const uint2 lo = *reinterpret_cast<const uint2*>(vrow + 4 * ((8 * u + q4) ^ sw));
-        const uint2 hi = *reinterpret_cast<const uint2*>(vrow + 4 * ((8 * u + 4 + q4) ^ sw));
-        const uint4 vf = make_uint4(lo.x, lo.y, hi.x, hi.y);
+        const uint4 vf = vfrag(S, u, dd);
 #pragma unroll
         for (int r = 0; r < RT; r++) O[r][dd] = mma32<MT>(vf, pb[r][u], O[r][dd]);
       }
@@ -542,11 +564,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       barrier();  // the slot's tile is in LDS; every wave is done with the previous tile's operands
       RawTile T;
       load_lds(S, T);
-      if (t0 >= klo && t0 + kKT <= khi) stage(t0, T, 0, std::false_type{});
-      else stage(t0, T, 0, std::true_type{});
+      if (t0 >= klo && t0 + kKT <= khi) stage(t0, T, std::false_type{});
+      else stage(t0, T, std::true_type{});
       barrier();  // operands ready; the slot is free
       if (t0 + 2 * kKT < khi) dma(t0 + 2 * kKT, S);
-      compute(t0, 0);
+      compute(t0, S);
     };
     dma(tfirst, raw0);
     if (tfirst + kKT < khi) dma(tfirst + kKT, raw1);
@@ -559,21 +581,57 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       if (t0 >= khi) break;
     }
   } else {
-    RawTile A, B;
-    load(tfirst, A);
-    stage(tfirst, A, 0, std::true_type{});
-    __syncthreads();
-    int buf = 0;
-    for (int t0 = tfirst; t0 < khi; t0 += kKT) {
-      const bool more = t0 + kKT < khi;
-      if (more) load(t0 + kKT, B);
-      compute(t0, buf);
-      if (more) {
-        if (t0 + kKT >= klo && t0 + 2 * kKT <= khi) stage(t0 + kKT, B, buf ^ 1, std::false_type{});
-        else stage(t0 + kKT, B, buf ^ 1, std::true_type{});
+    // 16-bit: wave w loads key rows 16 w .. 16 w + 15 of K and of V (4 instructions of 1 KB each), chunk c of
+    // row r to slot c ^ sw16(r)
+    constexpr int kWaitOne = (0xF << 8) | (0x7 << 4) | 8;  // vmcnt(8): the other slot's loads may stay in flight
+    constexpr int kWaitAll = (0xF << 8) | (0x7 << 4);
+    constexpr int kWaitLds = (0x3 << 14) | (0x7 << 4) | 0xF;
+    auto barrier = [&]() __attribute__((always_inline)) {
+      __builtin_amdgcn_s_waitcnt(kWaitLds);
+      __builtin_amdgcn_s_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+    };
+    auto dma16t = [&](int t0, uint8_t* S) __attribute__((always_inline)) {
+      const uint32_t ls = lds_addr(S);
+#pragma unroll
+      for (int u = 0; u < 4; u++) {
+        const int r = 16 * wave + 4 * u + (lane >> 4);
+        const uint32_t voff = uint32_t(t0 + r) * 256u + 16u * uint32_t((lane & 15) ^ sw16(r));
+        dma16(dk16, ls + 1024u * uint32_t(4 * wave + u), voff);
+        dma16(dv16, ls + 16384u + 1024u * uint32_t(4 * wave + u), voff);
       }
-      __syncthreads();
-      buf ^= 1;
+    };
+    // a tile reaching past [klo, khi): the V rows of keys outside it are cleared (rows past n or before start
+    // may hold anything, and 0 * inf is not 0); their K rows only give scores that the mask discards
+    auto clear_v = [&](int t0, uint8_t* S) __attribute__((always_inline)) {
+      const int key = tid >> 2, kg = t0 + key;
+      if (kg < klo || kg >= khi) {
+        uint4* row = reinterpret_cast<uint4*>(S + 16384 + key * 256 + 64 * (tid & 3));
+#pragma unroll
+        for (int i = 0; i < 4; i++) row[i] = make_uint4(0u, 0u, 0u, 0u);
+      }
+    };
+    auto step = [&](int t0, uint8_t* S) __attribute__((always_inline)) {
+      if (t0 + kKT < khi) __builtin_amdgcn_s_waitcnt(kWaitOne);
+      else __builtin_amdgcn_s_waitcnt(kWaitAll);
+      barrier();  // every wave's loads of this tile are in the slot
+      if (t0 < klo || t0 + kKT > khi) {
+        clear_v(t0, S);
+        barrier();
+      }
+      compute(t0, S);
+      barrier();  // every wave is done with the slot
+      if (t0 + 2 * kKT < khi) dma16t(t0 + 2 * kKT, S);
+    };
+    dma16t(tfirst, raw0);
+    if (tfirst + kKT < khi) dma16t(tfirst + kKT, raw1);
+    for (int t0 = tfirst;;) {
+      step(t0, raw0);
+      t0 += kKT;
+      if (t0 >= khi) break;
+      step(t0, raw1);
+      t0 += kKT;
+      if (t0 >= khi) break;
     }
   }
 
@@ -664,9 +722,9 @@ __global__ __launch_bounds__(256) void sdpa_combine(SdpaCombineParams p) {
 
 template <int QDT, int SDT, int FMT, int MT, int MASK>
 static void launch_rt(int rt, dim3 grid, hipStream_t s, hipEvent_t e0, hipEvent_t e1, const SdpaParams& p) {
-  // two row tiles only for 8-bit keys and values without a dense or window mask (their per-key tests for two
-  // tiles would not fit in registers)
-  if constexpr (FMT == KV_Q8 && MASK != MK_DENSE && MASK != MK_WINDOW) {
+  // two row tiles: 16-bit keys and values without a dense mask, 8-bit without a dense or window mask (their
+  // per-key tests for two tiles would not fit beside the staging registers)
+  if constexpr (MASK != MK_DENSE && (FMT == KV_16 || MASK != MK_WINDOW)) {
     if (rt == 2) {
       hipExtLaunchKernelGGL((sdpa_pass1<QDT, SDT, FMT, MT, MASK, 2>), grid, dim3(256), 0, s, e0, e1, 0, p);
       return;
@@ -749,11 +807,11 @@ int lcl_sdpa_ex(const void* q, int qdt, int kvfmt, const uint32_t* kw, const voi
   if (mask_kind == MK_WINDOW && window <= 0) return -1;
   if (mask_kind == MK_TREE && (!tree || L > 64 || L > N)) return -2;
   if (mask_kind == MK_DENSE && !dense) return -1;
-  // row tiles a wave: two (128 rows a workgroup) for 8-bit keys and values when there are more than 64 rows,
-  // halving the dequantization and the operand reads per row; one otherwise (16-bit needs no dequantization; the
-  // dense and window masks' per-key tests would not fit beside two tiles' registers)
+  // row tiles a wave: two (128 rows a workgroup) when there are more than 64 rows, halving the operand reads (and,
+  // 8-bit, the dequantization) per row; one under a dense mask, and for 8-bit under a window (their per-key
+  // tests would not fit beside two tiles' registers)
   const int rows = L * (H / KVH);
-  const int rt = (kvfmt == KV_Q8 && mask_kind != MK_DENSE && mask_kind != MK_WINDOW && rows > 64) ? 2 : 1;
+  const int rt = (rows > 64 && mask_kind != MK_DENSE && (kvfmt == KV_16 || mask_kind != MK_WINDOW)) ? 2 : 1;
   int chunk = sdpa_chunk(block, B, H, L, N, 64 * rt);
   int nchunks = N > 0 ? (N + chunk - 1) / chunk : 1;
   if (mask_kind == MK_WINDOW && N > 0) {
@@ -782,7 +840,9 @@ int lcl_sdpa_ex(const void* q, int qdt, int kvfmt, const uint32_t* kw, const voi
   p.nrowblocks = (rows + 64 * rt - 1) / (64 * rt);
   hipEvent_t e0 = static_cast<hipEvent_t>(ev_start), e1 = static_cast<hipEvent_t>(ev_stop);
   {  // with no key in reach every workgroup records empty parts, so the combine needs no cleared workspace
-    const dim3 grid(nchunks, p.nrowblocks, B * KVH);
+    const long long total = (long long)nchunks * p.nrowblocks * B * KVH;  // one-dimensional, mapped per XCD
+    if (total > (1LL << 30)) return -2;
+    const dim3 grid(unsigned((total + 7) / 8 * 8));
     if (kvfmt == KV_Q8) launch_fmt<KV_Q8>(qdt, kvdt, rt, grid, stream, e0, e1, p);
     else launch_fmt<KV_16>(qdt, kvdt, rt, grid, stream, e0, e1, p);
   }
