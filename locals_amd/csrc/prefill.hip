@@ -110,13 +110,6 @@ __device__ __forceinline__ f4 mma32(uint4 a, uint4 b, f4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, a), __builtin_bit_cast(h8, b), c, 0, 0, 0);
 }
 
-template <int DT>
-__device__ __forceinline__ float ldv(const void* p, size_t i) {
-  if constexpr (DT == DT_F32) return static_cast<const float*>(p)[i];
-  else if constexpr (DT == DT_BF16) return bf16_bits_to_f32(static_cast<const uint16_t*>(p)[i]);
-  else return f16_bits_to_f32(static_cast<const uint16_t*>(p)[i]);
-}
-
 // code pair (1024 + a, 1024 + b) -> scale * code + bias for fp16 scale/bias pairs: exact code, one fp16 rounding
 __device__ __forceinline__ uint32_t dq_h2(uint32_t codes1024, uint32_t sc2, uint32_t bi2) {
   const h2 c = __builtin_bit_cast(h2, codes1024) - h2{_Float16(1024.0f), _Float16(1024.0f)};
@@ -226,23 +219,38 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   __shared__ __attribute__((aligned(16))) uint8_t raw1[FMT == KV_Q8 ? kRawSlot : kRaw16];
 
   // Q^T as B operands: qb[r][kk] = scale log2(e) q[row][32 kk + 8 q4 + j], scaled in fp32 before its one rounding
-  // to the MFMA type, so the products come out as base-2 logits
+  // to the MFMA type, so the products come out as base-2 logits.  Loaded (16 bytes a lane a step) after the first
+  // tiles' loads are issued, so the two latencies overlap.
   uint4 qb[RT][4];
+  auto load_q = [&]() __attribute__((always_inline)) {
 #pragma unroll
-  for (int r = 0; r < RT; r++) {
-    const size_t qrow = ((size_t(b) * p.H + head[r]) * p.L + qi[r]) * kD;
+    for (int r = 0; r < RT; r++) {
+      const size_t qrow = ((size_t(b) * p.H + head[r]) * p.L + qi[r]) * kD;
 #pragma unroll
-    for (int kk = 0; kk < 4; kk++) {
-      float x[8];
+      for (int kk = 0; kk < 4; kk++) {
+        const size_t qo = qrow + 32 * kk + 8 * q4;
+        float x[8];
+        if constexpr (QDT == DT_F32) {
+          const float4 a = *reinterpret_cast<const float4*>(static_cast<const float*>(p.q) + qo);
+          const float4 c = *reinterpret_cast<const float4*>(static_cast<const float*>(p.q) + qo + 4);
+          x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w; x[4] = c.x; x[5] = c.y; x[6] = c.z; x[7] = c.w;
+        } else {
+          const uint4 w = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(p.q) + qo);
+          const uint32_t wv[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
-      for (int j = 0; j < 8; j++) x[j] = ldv<QDT>(p.q, qrow + 32 * kk + 8 * q4 + j) * p.scale_log2;
-      if (!real[r]) {
+          for (int i = 0; i < 4; i++) {
+            x[2 * i] = QDT == DT_BF16 ? bf16_bits_to_f32(uint16_t(wv[i])) : f16_bits_to_f32(uint16_t(wv[i]));
+            x[2 * i + 1] =
+                QDT == DT_BF16 ? bf16_bits_to_f32(uint16_t(wv[i] >> 16)) : f16_bits_to_f32(uint16_t(wv[i] >> 16));
+          }
+        }
 #pragma unroll
-        for (int j = 0; j < 8; j++) x[j] = 0.0f;
+        for (int j = 0; j < 8; j++) x[j] = real[r] ? x[j] * p.scale_log2 : 0.0f;
+        qb[r][kk] =
+            make_uint4(pack2<MT>(x[0], x[1]), pack2<MT>(x[2], x[3]), pack2<MT>(x[4], x[5]), pack2<MT>(x[6], x[7]));
       }
-      qb[r][kk] = make_uint4(pack2<MT>(x[0], x[1]), pack2<MT>(x[2], x[3]), pack2<MT>(x[4], x[5]), pack2<MT>(x[6], x[7]));
     }
-  }
+  };
 
   // buffers of this (row, kv head); loads past the capacity read 0
   const size_t tok0 = (size_t(b) * p.KVH + kvh) * p.cap;
@@ -572,6 +580,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     };
     dma(tfirst, raw0);
     if (tfirst + kKT < khi) dma(tfirst + kKT, raw1);
+    load_q();
     for (int t0 = tfirst;;) {
       step(t0, raw0);
       t0 += kKT;
@@ -625,6 +634,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     };
     dma16t(tfirst, raw0);
     if (tfirst + kKT < khi) dma16t(tfirst + kKT, raw1);
+    load_q();
     for (int t0 = tfirst;;) {
       step(t0, raw0);
       t0 += kKT;
