@@ -42,12 +42,8 @@ namespace lcl {
 constexpr int kD = 128;
 constexpr int kKT = 64;                 // keys a tile
 constexpr int kKsStride = 136;          // halves a K row in LDS (272 B: 16 B aligned, 4-bank skew a row)
-constexpr int kVtStride = 72;           // halves a V^T row in LDS (144 B: 36-bank skew a row)
 constexpr int kRawSlot = 8192 + 8192 + 1024;  // an 8-bit raw tile: K codes, V codes, ks / kb / vs / vb
 constexpr float kThr = 6.0f;
-// V^T row d keeps its 16 four-key slots XOR-permuted by (d >> 3) & 15: the staging writes, which take 8
-// consecutive rows a thread and rows 8 apart across a wave's lanes, then fall in distinct banks
-__device__ __forceinline__ int vt_swz(int d) { return (d >> 3) & 15; }
 // A 16-bit K + V tile (64 key rows of 256 B each).  Key row r keeps its 16-byte chunk c at slot c ^ sw16(r), a
 // permutation of r's low four bits: the K operand reads (16 rows, one chunk each) are then free of bank
 // conflicts and the transposing V reads (16 consecutive rows, two chunks each) two-way, the least for 512 B.
@@ -118,10 +114,8 @@ __device__ __forceinline__ uint32_t dq_h2(uint32_t codes1024, uint32_t sc2, uint
 
 // The raw bytes of one 64-key tile a thread stages (8-bit: codes + its keys' scale/bias; 16-bit: values)
 struct RawTile {
-  u4 k[4];         // K: 8-bit uses k[0..1] (32 codes of key tid/4), 16-bit k[0..3] (32 values)
-  u4 v[4];         // V: 8-bit uses v[k].xy (8 codes of key 4 kq + k), 16-bit v[k] (8 values)
-  uint32_t ks, kb; // K scale / bias (16-bit pair entry of the key's group) -- 8-bit only
-  uint32_t vs[4], vb[4];
+  u4 k[2], v[2];   // 32 K codes and 32 V codes of the thread's key (dims 32 kpart ..)
+  uint32_t ks, kb, vs, vb;  // the key's scale / bias pairs (one 16-bit entry a 64-dim group)
 };
 
 // Direct buffer -> LDS loads issued as asm, outside the compiler's LDS-DMA wait tracking (merged at a loop head it
@@ -210,11 +204,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   }
 
   // 8-bit: raw tiles arrive by direct buffer->LDS loads into two named slots (one in flight while the other is
-  // staged) and are dequantized into one operand buffer (Ks, Vt).  16-bit: the K and V tiles arrive the same way
+  // staged) and are dequantized into one operand buffer (Ks; Vk key-major as the 16-bit V region, read through the
+  // transposing read).  16-bit: the K and V tiles arrive the same way
   // (chunks swizzled by sw16) and are the MFMA operands themselves -- K rows read as they are, V^T through the
   // transposing read -- so nothing is staged.
   __shared__ __attribute__((aligned(16))) uint16_t Ks[FMT == KV_Q8 ? kKT * kKsStride : 8];
-  __shared__ __attribute__((aligned(16))) uint16_t Vt[FMT == KV_Q8 ? kD * kVtStride : 8];
+  __shared__ __attribute__((aligned(16))) uint8_t Vk[FMT == KV_Q8 ? kKT * 256 : 16];
   __shared__ __attribute__((aligned(16))) uint8_t raw0[FMT == KV_Q8 ? kRawSlot : kRaw16];
   __shared__ __attribute__((aligned(16))) uint8_t raw1[FMT == KV_Q8 ? kRawSlot : kRaw16];
 
@@ -269,8 +264,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   // 8-bit DMA: the scale / bias array this wave sends (wave 0 K scales, 1 K biases, 2 V scales, 3 V biases)
   const void* sarr = FMT != KV_Q8 ? p.kf : wave == 0 ? p.ks : wave == 1 ? p.kb : wave == 2 ? p.vs : p.vb;
   const BufRsrc rsw = make_rsrc(static_cast<const uint16_t*>(sarr) + tok0 * 2, cap * 4u);
-  const int kkey = tid >> 2, kpart = tid & 3;   // K staging: one key, 32 dims
-  const int vkq = tid >> 4, vdq = tid & 15;     // V staging: keys 4 vkq .. +3, dims 8 vdq .. +7
+  const int kkey = tid >> 2, kpart = tid & 3;   // staging: one key, 32 dims of its K and V
 
   // 8-bit raw tile in LDS: K codes (key-major 128 B rows, 8 KB), V codes (8 KB), ks / kb / vs / vb words (256 B
   // each).  Wave w sends K and V rows 16 w .. 16 w + 15 (two 1 KB pieces each) and the w-th scale array.
@@ -287,113 +281,54 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const uint8_t* kr = S + kkey * 128 + 32 * kpart;
     T.k[0] = *reinterpret_cast<const u4*>(kr);
     T.k[1] = *reinterpret_cast<const u4*>(kr + 16);
+    T.v[0] = *reinterpret_cast<const u4*>(kr + 8192);
+    T.v[1] = *reinterpret_cast<const u4*>(kr + 8192 + 16);
     T.ks = *reinterpret_cast<const uint32_t*>(S + 16384 + 4 * kkey);
     T.kb = *reinterpret_cast<const uint32_t*>(S + 16640 + 4 * kkey);
-#pragma unroll
-    for (int k = 0; k < 4; k++) {
-      const int vk = 4 * vkq + k;
-      const uint2 w = *reinterpret_cast<const uint2*>(S + 8192 + vk * 128 + 8 * vdq);
-      T.v[k] = u4{w.x, w.y, 0u, 0u};
-      T.vs[k] = *reinterpret_cast<const uint32_t*>(S + 16896 + 4 * vk);
-      T.vb[k] = *reinterpret_cast<const uint32_t*>(S + 17152 + 4 * vk);
-    }
+    T.vs = *reinterpret_cast<const uint32_t*>(S + 16896 + 4 * kkey);
+    T.vb = *reinterpret_cast<const uint32_t*>(S + 17152 + 4 * kkey);
   };
 
-  // dequantize an 8-bit tile into the operand buffer; keys outside [klo, khi) become 0
-  // (MASKED: the tile straddles an end of the range; otherwise every key is inside and no test is made)
+  // dequantize 32 codes (dims 32 kpart ..) with the key's scale / bias pair: 16 packed pairs of the MFMA type
+  auto dequant = [&](const u4 (&c)[2], uint32_t sc, uint32_t bi, uint32_t (&o)[16]) __attribute__((always_inline)) {
+    const uint32_t cw[8] = {c[0].x, c[0].y, c[0].z, c[0].w, c[1].x, c[1].y, c[1].z, c[1].w};
+    const int gsel = kpart >> 1;  // group of dims 32 kpart .. + 32
+    if constexpr (MT == DT_F16) {
+      const uint32_t s1 = (sc >> (16 * gsel)) & 0xffffu, b1 = (bi >> (16 * gsel)) & 0xffffu;
+      const uint32_t s2 = s1 | (s1 << 16), b2 = b1 | (b1 << 16);
+#pragma unroll
+      for (int w = 0; w < 8; w++) {
+        o[2 * w] = dq_h2(codes_to_h2(cw[w], 0x00050004u), s2, b2);
+        o[2 * w + 1] = dq_h2(codes_to_h2(cw[w], 0x00070006u), s2, b2);
+      }
+    } else {
+      const float sf = half_of(sc, gsel, SDT), bf = half_of(bi, gsel, SDT);
+#pragma unroll
+      for (int w = 0; w < 8; w++) {
+        o[2 * w] = pack2<MT>(sf * float(cw[w] & 0xffu) + bf, sf * float((cw[w] >> 8) & 0xffu) + bf);
+        o[2 * w + 1] = pack2<MT>(sf * float((cw[w] >> 16) & 0xffu) + bf, sf * float(cw[w] >> 24) + bf);
+      }
+    }
+  };
+  // dequantize an 8-bit tile into the operand buffers: K rows into Ks, V rows into Vk (16-byte chunk c of key r at
+  // slot c ^ sw16(r)); keys outside [klo, khi) become 0 (MASKED: the tile straddles an end of the range;
+  // otherwise every key is inside and no test is made)
   auto stage = [&](int t0, const RawTile& T, auto masked) __attribute__((always_inline)) {
     constexpr bool MASKED = decltype(masked)::value;
-    {
-      const int kg = t0 + kkey;
-      const bool kin = !MASKED || (kg >= klo && kg < khi);
-      uint32_t o[16];
-      if constexpr (FMT == KV_Q8) {
-        const uint32_t cw[8] = {T.k[0].x, T.k[0].y, T.k[0].z, T.k[0].w, T.k[1].x, T.k[1].y, T.k[1].z, T.k[1].w};
-        const int gsel = kpart >> 1;  // group of dims 32 kpart .. + 32
-        if constexpr (MT == DT_F16) {
-          const uint32_t s = (T.ks >> (16 * gsel)) & 0xffffu, bb = (T.kb >> (16 * gsel)) & 0xffffu;
-          const uint32_t s2 = s | (s << 16), b2 = bb | (bb << 16);
+    const int kg = t0 + kkey;
+    const bool kin = !MASKED || (kg >= klo && kg < khi);
+    uint32_t o[16];
+    dequant(T.k, T.ks, T.kb, o);
+    uint4* kdst = reinterpret_cast<uint4*>(&Ks[kkey * kKsStride + kpart * 32]);
 #pragma unroll
-          for (int w = 0; w < 8; w++) {
-            o[2 * w] = dq_h2(codes_to_h2(cw[w], 0x00050004u), s2, b2);
-            o[2 * w + 1] = dq_h2(codes_to_h2(cw[w], 0x00070006u), s2, b2);
-          }
-        } else {
-          const float sf = half_of(T.ks, gsel, SDT), bf = half_of(T.kb, gsel, SDT);
+    for (int u = 0; u < 4; u++)
+      kdst[u] = kin ? make_uint4(o[4 * u], o[4 * u + 1], o[4 * u + 2], o[4 * u + 3]) : make_uint4(0u, 0u, 0u, 0u);
+    dequant(T.v, T.vs, T.vb, o);
+    const int sw = sw16(kkey);
 #pragma unroll
-          for (int w = 0; w < 8; w++) {
-            o[2 * w] = pack2<MT>(sf * float(cw[w] & 0xffu) + bf, sf * float((cw[w] >> 8) & 0xffu) + bf);
-            o[2 * w + 1] = pack2<MT>(sf * float((cw[w] >> 16) & 0xffu) + bf, sf * float(cw[w] >> 24) + bf);
-          }
-        }
-      }
-      uint4* dst = reinterpret_cast<uint4*>(&Ks[kkey * kKsStride + kpart * 32]);
-#pragma unroll
-      for (int u = 0; u < 4; u++)
-        dst[u] = kin ? make_uint4(o[4 * u], o[4 * u + 1], o[4 * u + 2], o[4 * u + 3]) : make_uint4(0u, 0u, 0u, 0u);
-    }
-    {
-      bool vin[4];
-#pragma unroll
-      for (int k = 0; k < 4; k++) {
-        const int kg = t0 + 4 * vkq + k;
-        vin[k] = !MASKED || (kg >= klo && kg < khi);
-      }
-      uint32_t pr[8][2];  // dims 8 vdq + e: (keys 0,1), (keys 2,3)
-      if constexpr (FMT == KV_Q8) {
-        if constexpr (MT == DT_F16) {
-          const int gsel = vdq >> 3;
-          uint32_t s01, s23, b01, b23;
-          {
-            const uint32_t s0 = (T.vs[0] >> (16 * gsel)) & 0xffffu, s1 = (T.vs[1] >> (16 * gsel)) & 0xffffu;
-            const uint32_t s2 = (T.vs[2] >> (16 * gsel)) & 0xffffu, s3 = (T.vs[3] >> (16 * gsel)) & 0xffffu;
-            const uint32_t b0 = (T.vb[0] >> (16 * gsel)) & 0xffffu, b1 = (T.vb[1] >> (16 * gsel)) & 0xffffu;
-            const uint32_t b2 = (T.vb[2] >> (16 * gsel)) & 0xffffu, b3 = (T.vb[3] >> (16 * gsel)) & 0xffffu;
-            s01 = s0 | (s1 << 16); s23 = s2 | (s3 << 16); b01 = b0 | (b1 << 16); b23 = b2 | (b3 << 16);
-          }
-#pragma unroll
-          for (int h = 0; h < 2; h++) {  // dwords: dims 8 vdq + 4 h .. + 3
-            const uint32_t w0 = h ? T.v[0].y : T.v[0].x, w1 = h ? T.v[1].y : T.v[1].x;
-            const uint32_t w2 = h ? T.v[2].y : T.v[2].x, w3 = h ? T.v[3].y : T.v[3].x;
-            const uint32_t x01 = __builtin_amdgcn_perm(w1, w0, 0x05010400u), y01 = __builtin_amdgcn_perm(w1, w0, 0x07030602u);
-            const uint32_t x23 = __builtin_amdgcn_perm(w3, w2, 0x05010400u), y23 = __builtin_amdgcn_perm(w3, w2, 0x07030602u);
-            pr[4 * h + 0][0] = dq_h2(codes_to_h2(x01, 0x00050004u), s01, b01);
-            pr[4 * h + 1][0] = dq_h2(codes_to_h2(x01, 0x00070006u), s01, b01);
-            pr[4 * h + 2][0] = dq_h2(codes_to_h2(y01, 0x00050004u), s01, b01);
-            pr[4 * h + 3][0] = dq_h2(codes_to_h2(y01, 0x00070006u), s01, b01);
-            pr[4 * h + 0][1] = dq_h2(codes_to_h2(x23, 0x00050004u), s23, b23);
-            pr[4 * h + 1][1] = dq_h2(codes_to_h2(x23, 0x00070006u), s23, b23);
-            pr[4 * h + 2][1] = dq_h2(codes_to_h2(y23, 0x00050004u), s23, b23);
-            pr[4 * h + 3][1] = dq_h2(codes_to_h2(y23, 0x00070006u), s23, b23);
-          }
-        } else {
-          const int gsel = vdq >> 3;
-          float sf[4], bf[4];
-#pragma unroll
-          for (int k = 0; k < 4; k++) {
-            sf[k] = half_of(T.vs[k], gsel, SDT);
-            bf[k] = half_of(T.vb[k], gsel, SDT);
-          }
-#pragma unroll
-          for (int e = 0; e < 8; e++) {
-            float v[4];
-#pragma unroll
-            for (int k = 0; k < 4; k++) {
-              const uint32_t w = e < 4 ? T.v[k].x : T.v[k].y;
-              v[k] = sf[k] * float((w >> (8 * (e & 3))) & 0xffu) + bf[k];
-            }
-            pr[e][0] = pack2<MT>(v[0], v[1]);
-            pr[e][1] = pack2<MT>(v[2], v[3]);
-          }
-        }
-      }
-      const uint32_t m01 = (vin[0] ? 0xffffu : 0u) | (vin[1] ? 0xffff0000u : 0u);
-      const uint32_t m23 = (vin[2] ? 0xffffu : 0u) | (vin[3] ? 0xffff0000u : 0u);
-#pragma unroll
-      for (int e = 0; e < 8; e++)
-        *reinterpret_cast<uint2*>(&Vt[(8 * vdq + e) * kVtStride + 4 * (vkq ^ vt_swz(8 * vdq + e))]) =
-            make_uint2(pr[e][0] & m01, pr[e][1] & m23);
-    }
+    for (int u = 0; u < 4; u++)
+      *reinterpret_cast<uint4*>(&Vk[kkey * 256 + 16 * ((4 * kpart + u) ^ sw)]) =
+          kin ? make_uint4(o[4 * u], o[4 * u + 1], o[4 * u + 2], o[4 * u + 3]) : make_uint4(0u, 0u, 0u, 0u);
   };
 
   float m_run[RT], l_acc[RT];
@@ -422,7 +357,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   // its 8 values are dim 16 dd + m of the keys whose P^T the B operand holds at k = 8 q4 + j.
   const int sk16 = sw16(c16);
   const int vkey16 = 4 * q4 + (c16 >> 2), vsw16 = sw16(vkey16);
-  const int vch16 = (c16 & 3) >> 1, voff16 = 16384 + vkey16 * 256 + 8 * (c16 & 1);
+  const int vch16 = (c16 & 3) >> 1, voff16 = vkey16 * 256 + 8 * (c16 & 1);
   auto kfrag = [&](const uint8_t* S, int t, int kk) __attribute__((always_inline)) -> uint4 {
     if constexpr (FMT == KV_Q8)
       return *reinterpret_cast<const uint4*>(&Ks[(16 * t + c16) * kKsStride + 8 * q4 + 32 * kk]);
@@ -430,17 +365,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       return *reinterpret_cast<const uint4*>(S + (16 * t + c16) * 256 + 16 * ((4 * kk + q4) ^ sk16));
   };
   auto vfrag = [&](const uint8_t* S, int u, int dd) __attribute__((always_inline)) -> uint4 {
-    if constexpr (FMT == KV_Q8) {
-      const int vr = 16 * dd + c16, sw = vt_swz(vr);
-      const uint16_t* vrow = &Vt[vr * kVtStride];
-      const uint2 lo = *reinterpret_cast<const uint2*>(vrow + 4 * ((8 * u + q4) ^ sw));
-      const uint2 hi = *reinterpret_cast<const uint2*>(vrow + 4 * ((8 * u + 4 + q4) ^ sw));
-      return make_uint4(lo.x, lo.y, hi.x, hi.y);
-    } else {
-      const uint8_t* a = S + voff16 + 32 * u * 256 + 16 * ((2 * dd + vch16) ^ vsw16);
-      const uint2 lo = lds_read_tr16(a), hi = lds_read_tr16(a + 16 * 256);
-      return make_uint4(lo.x, lo.y, hi.x, hi.y);
-    }
+    // the V region: the slot's second half (16-bit), the dequantized buffer Vk (8-bit), the same layout
+    const uint8_t* a = (FMT == KV_Q8 ? Vk : S + 16384) + voff16 + 32 * u * 256 + 16 * ((2 * dd + vch16) ^ vsw16);
+    const uint2 lo = lds_read_tr16(a), hi = lds_read_tr16(a + 16 * 256);
+    return make_uint4(lo.x, lo.y, hi.x, hi.y);
   };
 
   // Each K / V^T operand fragment is read from LDS once and applied to every row tile of the wave, so a
