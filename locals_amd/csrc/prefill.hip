@@ -267,22 +267,27 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const int kkey = tid >> 2, kpart = tid & 3;   // staging: one key, 32 dims of its K and V
 
   // 8-bit raw tile in LDS: K codes (key-major 128 B rows, 8 KB), V codes (8 KB), ks / kb / vs / vb words (256 B
-  // each).  Wave w sends K and V rows 16 w .. 16 w + 15 (two 1 KB pieces each) and the w-th scale array.
+  // each).  Wave w sends K and V rows 16 w .. 16 w + 15 (two 1 KB pieces each) and the w-th scale array.  Row r
+  // keeps its 16-byte chunk c at slot c ^ ((r >> 1) & 1), so the staging reads (32 bytes of each of 16 rows a
+  // wave) cover every bank group.
   auto dma = [&](int t0, uint8_t* S) __attribute__((always_inline)) {
-    const uint32_t base = uint32_t(t0) * 128u + uint32_t(wave) * 2048u + 16u * uint32_t(lane);
-    lds_load16(rk, S + 2048 * wave, base);
-    lds_load16(rk, S + 2048 * wave + 1024, base + 1024u);
-    lds_load16(rv, S + 8192 + 2048 * wave, base);
-    lds_load16(rv, S + 8192 + 2048 * wave + 1024, base + 1024u);
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+      const int r = 16 * wave + 8 * i + (lane >> 3);
+      const uint32_t voff = uint32_t(t0 + r) * 128u + 16u * uint32_t((lane & 7) ^ ((r >> 1) & 1));
+      lds_load16(rk, S + 2048 * wave + 1024 * i, voff);
+      lds_load16(rv, S + 8192 + 2048 * wave + 1024 * i, voff);
+    }
     lds_load4(rsw, S + 16384 + 256 * wave, (uint32_t(t0) + uint32_t(lane)) * 4u);
   };
   // the thread's share of a raw tile in LDS, as the register-prefetch path would hold it
   auto load_lds = [&](const uint8_t* S, RawTile& T) __attribute__((always_inline)) {
+    const int f = (kkey >> 1) & 1;  // the row's chunk swizzle: chunks 2 kpart, 2 kpart + 1 at slots c ^ f
     const uint8_t* kr = S + kkey * 128 + 32 * kpart;
-    T.k[0] = *reinterpret_cast<const u4*>(kr);
-    T.k[1] = *reinterpret_cast<const u4*>(kr + 16);
-    T.v[0] = *reinterpret_cast<const u4*>(kr + 8192);
-    T.v[1] = *reinterpret_cast<const u4*>(kr + 8192 + 16);
+    T.k[0] = *reinterpret_cast<const u4*>(kr + 16 * f);
+    T.k[1] = *reinterpret_cast<const u4*>(kr + 16 * (f ^ 1));
+    T.v[0] = *reinterpret_cast<const u4*>(kr + 8192 + 16 * f);
+    T.v[1] = *reinterpret_cast<const u4*>(kr + 8192 + 16 * (f ^ 1));
     T.ks = *reinterpret_cast<const uint32_t*>(S + 16384 + 4 * kkey);
     T.kb = *reinterpret_cast<const uint32_t*>(S + 16640 + 4 * kkey);
     T.vs = *reinterpret_cast<const uint32_t*>(S + 16896 + 4 * kkey);
