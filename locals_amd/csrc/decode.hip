@@ -7,8 +7,17 @@
 // (ragged_attention: row r reads KV slot slots[r], keys [0, nkeys[r]), no sink,
 // 0 for an empty row).
 //
-// MI355X design (one pass-1 workgroup = 4 waves = one (row, kv head, head slice,
-// key chunk); each wave streams a quarter of the chunk in tiles of 16 keys):
+// Pass-1 kernels (the host picks one; pass 2, decode_combine, joins their parts):
+//  * qkv_pass1_q8_quad (8-bit, G <= 4): stream-K over all (row,
+//    kv head, 64-key tile) work, one wave a workgroup, tiles by direct buffer->LDS
+//    loads, Q K^T on the 4x4x4 MFMA so no lane computes a padding head; described
+//    where it is defined.
+//  * qkv_pass1_q8 (8-bit, G > 4), below; qkv_pass1_q8_lds an LDS-staged form of it,
+//    kept for comparisons (LOCALS_AMD_DECODE=lds).
+//  * ragged_pass1_16 (16-bit K/V, ragged rows).
+//
+// qkv_pass1_q8 (one workgroup = 4 waves = one (row, kv head, head slice, key
+// chunk); each wave streams a quarter of the chunk in tiles of 16 keys):
 //  * Q K^T on MFMA 16x16x16 f16: A = 16 keys x 16 dims of codes turned into exact
 //    fp16 (1024 + code) by one v_perm per two codes, B = Q^T with the G query
 //    heads of the kv head in the 16 columns (one key tile is read once for all of

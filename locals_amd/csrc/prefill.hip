@@ -13,13 +13,13 @@
 //    the reference slices the keys a band of queries reaches, here each workgroup reads only its rows' band;
 //  * the sink is a logit in the denominator only.
 //
-// MI355X design.  Grid (key chunk, row block, row x kv head); a workgroup = 4 waves =
-// 64 rows, a row being one (query, head) of the kv head's G heads (row r: query r / G,
-// head r % G, so any G works).  Per 64-key tile the workgroup dequantizes K and V once
-// into LDS as MFMA operands (fp32 scale * code + bias, rounded once to the MFMA type,
-// as the reference's dequantized() feeds its attention in T) -- K row-major and V
-// transposed, rows padded so the operand reads are bank-conflict free -- and every wave
-// reuses the tile for its 16 rows:
+// MI355X design.  Work units (key chunk, row block, batch row x kv head), dealt to the
+// XCDs in contiguous runs; a workgroup = 4 waves = 64 or 128 rows (one or two 16-row
+// tiles a wave), a row being one (query, head) of the kv head's G heads (row r: query
+// r / G, head r % G, so any G works).  Per 64-key tile: 8-bit K and V are dequantized
+// once into LDS as MFMA operands (fp32 scale * code + bias, rounded once to the MFMA
+// type, as the reference's dequantized() feeds its attention in T); 16-bit tiles are the
+// operands as loaded.  Every wave reuses the tile for its rows:
 //  * S^T = K Q^T on v_mfma_f32_16x16x32 (A = 16 keys x 32 dims from LDS, B = Q^T from
 //    registers): lane l gets S[row l % 16][keys 4 (l / 16) + i] -- the softmax state of
 //    a row lives in one lane column, its max needs two cross-lane steps;
