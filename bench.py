@@ -1,6 +1,6 @@
 """Benchmark of the batched-attention hot path on one MI355X: 8-bit-KV GQA flash-decode.
 
-    python bench.py [--steps K] [--warmup W] [--config c2|c3|c4|c5|w1] [--cpu-seconds S] [--no-cpu]
+    python bench.py [--steps K] [--warmup W] [--config c2|c1|c3|c4|c5|w1|f2] [--cpu-seconds S] [--no-cpu]
 
 A step is one ``qkv.attend`` over the whole batch (pass 1 + the log-sum-exp combine) with K/V already resident in
 HBM.  Workload (default, "c2"): B=16 rows, 32 query / 8 KV heads, head_dim 128, row contexts n_b ~ U[1024, 32768]
@@ -80,6 +80,11 @@ def config(name: str, seed: int = 0):
         nb = g.integers(1024, 32768, size=B, endpoint=True)
         return dict(name="c2", workload="8-bit KV GQA flash-decode, mixed contexts (BASELINE config 2)",
                     B=B, H=H, KVH=KVH, nb=nb)
+    if name == "f2":
+        B, H, KVH = 16, 32, 4
+        nb = g.integers(1024, 32768, size=B, endpoint=True)
+        return dict(name="f2", workload="8-bit KV flash-decode with Flint's head layout (32 query / 4 KV heads, G = 8), "
+                    "the rows and contexts of BASELINE config 2", B=B, H=H, KVH=KVH, nb=nb)
     if name == "c3":
         return dict(name="c3", workload="long-context single-row split-K decode (BASELINE config 3)",
                     B=1, H=16, KVH=8, nb=np.array([245760]))

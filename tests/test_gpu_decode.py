@@ -2,7 +2,7 @@
 
 Cases follow the reference's own test (tests/test_flint.py:278-295: (B, n, cap, pads) =
 (1,1,256,[0]), (1,13,256,[0]), (1,2100,2304,[0]), (3,700,768,[0,37,300]), K ~ 2 N(0,1), sinks ~ 2 N(0,1), scale
-0.0884) over the head layouts (32,4) and (4,2) it uses plus the BASELINE shapes (32/8, 16/8) and G = 1, 16, 32.
+0.0884) over the head layouts (32,4) and (4,2) it uses plus the BASELINE shapes (32/8, 16/8) and G = 1, 6, 16, 32.
 Bar: max |got - oracle| <= 2e-3 for fp16 outputs; bf16 uses the reference's 2^-7 (1 + max|ref|).
 """
 
@@ -16,7 +16,7 @@ from tests.inputs import normal16, q8_cache, rng, to_torch, triple_to_torch
 pytestmark = pytest.mark.gpu
 
 CASES = [(1, 1, 256, [0]), (1, 13, 256, [0]), (1, 2100, 2304, [0]), (3, 700, 768, [0, 37, 300])]
-HEADS = [(32, 4), (4, 2), (32, 8), (16, 8), (8, 8), (16, 1), (32, 1)]
+HEADS = [(32, 4), (24, 4), (4, 2), (32, 8), (16, 8), (8, 8), (16, 1), (32, 1)]
 
 
 def _out(t):
