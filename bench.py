@@ -1,6 +1,6 @@
 """Benchmark of the batched-attention hot path on one MI355X: 8-bit-KV GQA flash-decode.
 
-    python bench.py [--steps K] [--warmup W] [--config c2|c1|c3|c4|c5|w1|f2] [--cpu-seconds S] [--no-cpu]
+    python bench.py [--steps K] [--warmup W] [--config c2|c1|c3|c4|c5|w1|f2|qk] [--cpu-seconds S] [--no-cpu]
 
 A step is one ``qkv.attend`` over the whole batch (pass 1 + the log-sum-exp combine) with K/V already resident in
 HBM.  Workload (default, "c2"): B=16 rows, 32 query / 8 KV heads, head_dim 128, row contexts n_b ~ U[1024, 32768]
@@ -80,6 +80,9 @@ def config(name: str, seed: int = 0):
         nb = g.integers(1024, 32768, size=B, endpoint=True)
         return dict(name="c2", workload="8-bit KV GQA flash-decode, mixed contexts (BASELINE config 2)",
                     B=B, H=H, KVH=KVH, nb=nb)
+    if name == "qk":
+        return dict(name="qk", workload="qk_norm_rope, quantize_append and the fused qk_norm_rope_append at C2's "
+                    "decode step (16 x 1 token) and at a 512-token prompt chunk, 32 / 8 heads, bf16")
     if name == "f2":
         B, H, KVH = 16, 32, 4
         nb = g.integers(1024, 32768, size=B, endpoint=True)
@@ -282,6 +285,80 @@ def bench_c1(cfg, args, dev):
             "buffer_sets": nsets}
 
 
+def bench_qk(args, dev):
+    """The per-step kernels around attention in Flint's full-attention layers, at C2's decode step (16 rows x 1
+    token) and at a 512-token prompt chunk, 32 / 8 heads: qk_norm_rope (q/k norms + RoPE, v split out),
+    quantize_append (8-bit cache store of k and v) and the fused qk_norm_rope_append.  Each is one launch; the bytes
+    are what the call must move: bf16 activations in and out, 272 B of cache a token and kv head.  The calls are replayed from a HIP
+    graph of 20, so the time per call is the GPU's (with the gaps between the graph's launches), not the host's."""
+    import types
+
+    import torch
+
+    from locals_amd import _lib, qk_kernel, qkv
+
+    H, KV, HD = 32, 8, 128
+    res = {}
+    for name, B, L in (("decode_step", 16, 1), ("prompt_chunk", 1, 512)):
+        gen = torch.Generator(device=dev)
+        gen.manual_seed(5)
+        dt = torch.bfloat16
+        x = torch.randn((B, L, (H + 2 * KV) * HD), generator=gen, device=dev, dtype=dt)
+        wq = (torch.randn(HD, generator=gen, device=dev) * 0.05 + 1).to(dt)
+        wk = (torch.randn(HD, generator=gen, device=dev) * 0.05 + 1).to(dt)
+        attn = types.SimpleNamespace(n_heads=H, n_kv_heads=KV, head_dim=HD,
+                                     q_norm=types.SimpleNamespace(weight=wq, eps=1e-6),
+                                     k_norm=types.SimpleNamespace(weight=wk, eps=1e-6),
+                                     rope=types.SimpleNamespace(base=10000.0, dims=HD, traditional=False, scale=1.0))
+        offs = torch.full((B,), 1000, dtype=torch.int32, device=dev)
+        cap = 1024 + L
+        K = qkv._zeros(B, KV, cap, HD, dt, dev)
+        V = qkv._zeros(B, KV, cap, HD, dt, dev)
+        q, k, v = qk_kernel.qk_norm_rope(x, attn, offs)
+        lib = _lib.load()
+        P = _lib.ptr
+        qo = torch.empty((B, H, L, HD), dtype=dt, device=dev)
+
+        def fused():  # the stream is read at each call: under capture it is the capturing one
+            rc = lib.lcl_qk_norm_rope_append(P(x), 1, P(wq), P(wk), P(offs), 1, 1e-6, float(np.log2(10000.0)), 1, B, L,
+                                             H, KV, HD, P(qo), P(K[0]), P(K[1]), P(K[2]), P(V[0]), P(V[1]), P(V[2]),
+                                             cap, 1000, 0, _lib.stream_of(dev))
+            _lib.check(rc, "lcl_qk_norm_rope_append")
+
+        act = B * L * (H + 2 * KV) * HD * 2  # bf16 qkv
+        cache = B * L * KV * 272  # K and V triples
+        calls = {
+            "qk_norm_rope": (lambda: qk_kernel.qk_norm_rope(x, attn, offs), 2 * act),
+            "quantize_append": (lambda: qkv.quantize_into(k, v, K, V, 1000), B * L * KV * HD * 2 * 2 + cache),
+            "qk_norm_rope_append": (fused, act + B * L * H * HD * 2 + cache),
+        }
+        out = {}
+        per_graph = 20
+        for cname, (fn, nbytes) in calls.items():
+            for _ in range(args.warmup):
+                fn()
+            torch.cuda.synchronize()
+            # 20 calls captured in one HIP graph, so the host's launch cost is not what is timed
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                for _ in range(per_graph):
+                    fn()
+            g.replay()
+            torch.cuda.synchronize()
+            reps = max(1, args.steps // per_graph)
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(reps):
+                g.replay()
+            e1.record()
+            torch.cuda.synchronize()
+            us = e0.elapsed_time(e1) * 1e3 / (reps * per_graph)
+            out[cname] = {"us_per_call": round(us, 2), "bytes": nbytes, "GBs": round(nbytes / us / 1e3, 1),
+                          "hbm_frac": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4)}
+        res[name] = {"B": B, "L": L, **out}
+    return res
+
+
 def build_sets(cfg, nsets, dev):
     import torch
 
@@ -400,6 +477,9 @@ def main():
         qkv.BLOCK = args.block
     if cfg["name"] == "c1":
         print(json.dumps({"config": cfg["workload"], "ragged_decode": bench_c1(cfg, args, dev)}), flush=True)
+        return
+    if cfg["name"] == "qk":
+        print(json.dumps({"config": cfg["workload"], "qk_and_cache_store": bench_qk(args, dev)}), flush=True)
         return
     if cfg["name"] in ("c4", "c5", "w1"):
         from locals_amd import sdpa

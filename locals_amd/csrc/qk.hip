@@ -21,8 +21,9 @@
 // BatchQuantizedKVCache.update_and_fetch (locals/qkv.py:309-326) does with qk_norm_rope's k, v
 // (locals/fuse.py:80-83), without the 16-bit k and v ever reaching HBM.
 //
-// MI355X mapping: one workgroup (256 lanes) a token.  The HD/2 (cos, sin) pairs depend only on
-// the token's position, so the workgroup computes them once (fp64, in LDS) for all its heads.
+// MI355X mapping: one workgroup (256 lanes) a token, or a token's heads over several workgroups
+// when there are few tokens.  The HD/2 (cos, sin) pairs depend only on the token's position, so
+// a workgroup computes them once (fp64, in LDS) for all its heads.
 // A head is a 32-lane half-wave: lane j holds elements 2j, 2j + 1 (+ 64 p) of each half, one
 // 32-bit load each, and its RoPE partners in the other half, so a rotation never leaves the
 // lane.  Sums and group min/max reduce over the half-wave with xor shuffles.  HBM-bound:
@@ -134,6 +135,21 @@ __global__ __launch_bounds__(256) void qk_norm_rope_k(QkParams p) {
   __shared__ double s_cos[HALF], s_sin[HALF];
   const int bl = blockIdx.x;
   const int b = bl / p.L, l = bl % p.L;
+  const int hw = threadIdx.x >> 5, j = threadIdx.x & 31;
+  const int NH = p.H + 2 * p.KV;
+  const uint16_t* src_tok = p.qkv + size_t(bl) * NH * HD;
+  // a head's values, loaded one head ahead (the first before the (cos, sin) table, whose fp64 sincos is slow)
+  uint32_t nlo[PER], nhi[PER];
+  auto load_head = [&](int head) {
+    const uint16_t* src = src_tok + size_t(head) * HD;
+#pragma unroll
+    for (int q = 0; q < PER; q++) {
+      nlo[q] = *reinterpret_cast<const uint32_t*>(src + 2 * (32 * q + j));
+      nhi[q] = *reinterpret_cast<const uint32_t*>(src + HALF + 2 * (32 * q + j));
+    }
+  };
+  const int head0 = hw + 8 * int(blockIdx.y), hstep = 8 * int(gridDim.y);
+  if (head0 < NH) load_head(head0);
   if (ROPE) {
     const float pos = float(p.offsets[p.per_row ? b : 0] + l);
     for (int i = threadIdx.x; i < HALF; i += 256) {
@@ -148,17 +164,14 @@ __global__ __launch_bounds__(256) void qk_norm_rope_k(QkParams p) {
     }
     __syncthreads();
   }
-  const int hw = threadIdx.x >> 5, j = threadIdx.x & 31;
-  const int NH = p.H + 2 * p.KV;
-  const uint16_t* src_tok = p.qkv + size_t(bl) * NH * HD;
-  for (int head = hw; head < NH; head += 8) {
-    const uint16_t* src = src_tok + size_t(head) * HD;
+  for (int head = head0; head < NH; head += hstep) {
     uint32_t rlo[PER], rhi[PER];
 #pragma unroll
     for (int q = 0; q < PER; q++) {
-      rlo[q] = *reinterpret_cast<const uint32_t*>(src + 2 * (32 * q + j));
-      rhi[q] = *reinterpret_cast<const uint32_t*>(src + HALF + 2 * (32 * q + j));
+      rlo[q] = nlo[q];
+      rhi[q] = nhi[q];
     }
+    if (head + hstep < NH) load_head(head + hstep);
     if (head >= p.H + p.KV) {  // v
       const int kvh = head - p.H - p.KV;
       const size_t row = (size_t(b) * p.KV + kvh) * (FUSED ? p.cap : p.L) + (FUSED ? p.prev + l : l);
@@ -231,9 +244,14 @@ __global__ __launch_bounds__(256) void qk_norm_rope_k(QkParams p) {
   }
 }
 
+// Grid (token, head split): a token's heads go 8 at a time to gridDim.y workgroups until the grid has ~2048 of
+// them (8 a CU), so a decode step or a prompt chunk spreads over the CUs with few heads a workgroup in turn; each
+// workgroup computes its token's (cos, sin).
 template <int DT, int PER, bool FUSED>
 static void launch_rope(bool rope, const QkParams& p, hipStream_t s) {
-  const dim3 grid(p.B * p.L);
+  const int tokens = p.B * p.L, groups = (p.H + 2 * p.KV + 7) / 8;
+  const int split = min(groups, max(1, (2048 + tokens - 1) / tokens));
+  const dim3 grid(tokens, split);
   if (rope) hipLaunchKernelGGL((qk_norm_rope_k<DT, PER, true, FUSED>), grid, dim3(256), 0, s, p);
   else hipLaunchKernelGGL((qk_norm_rope_k<DT, PER, false, FUSED>), grid, dim3(256), 0, s, p);
 }
