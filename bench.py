@@ -533,8 +533,8 @@ def main():
     ev.close()
 
     ms_step = region_ms / K_
-    # the pass-1 kernel the library runs for this head ratio (4x4x4-MFMA stream-K kernel for G <= 4)
-    kernel = "qkv_pass1_q8_quad" if H // KVH <= 4 else "qkv_pass1_q8"
+    # the pass-1 kernel the library runs for this head ratio (4x4x4-MFMA stream-K kernel for G <= 8)
+    kernel = "qkv_pass1_q8_quad" if H // KVH <= 8 else "qkv_pass1_q8"
     b_step, b_p1 = step_bytes(cfg)
     value = b_step / (ms_step * 1e-3) / 1e9
     p1_us = float(p1.mean() * 1e3)

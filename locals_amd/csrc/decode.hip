@@ -8,11 +8,11 @@
 // 0 for an empty row).
 //
 // Pass-1 kernels (the host picks one; pass 2, decode_combine, joins their parts):
-//  * qkv_pass1_q8_quad (8-bit, G <= 4): stream-K over all (row,
-//    kv head, 64-key tile) work, one wave a workgroup, tiles by direct buffer->LDS
-//    loads, Q K^T on the 4x4x4 MFMA so no lane computes a padding head; described
-//    where it is defined.
-//  * qkv_pass1_q8 (8-bit, G > 4), below; qkv_pass1_q8_lds an LDS-staged form of it,
+//  * qkv_pass1_q8_quad (8-bit, G <= 8: BASELINE configs 2-4 and Flint's G = 8): stream-K
+//    over all (row, kv head, 64-key tile) work, one wave a workgroup, tiles by direct
+//    buffer->LDS loads, Q K^T on the 4x4x4 MFMA so no lane computes a padding head (one
+//    or two groups of 4 heads); described where it is defined.
+//  * qkv_pass1_q8 (8-bit, G > 8), below; qkv_pass1_q8_lds an LDS-staged form of it,
 //    kept for comparisons (LOCALS_AMD_DECODE=lds).
 //  * ragged_pass1_16 (16-bit K/V, ragged rows).
 //
@@ -643,7 +643,7 @@ __global__ __launch_bounds__(256) void qkv_pass1_q8_lds(DecodeParams p) {
   join_waves(p, s_m, s_l, s_o, Gs, r, head0, c);
 }
 
-// ------------------------------------------- 8-bit pass 1 for G <= 4 (quad)
+// ------------------------------------------- 8-bit pass 1 for G <= 8 (quad)
 // With 4 or fewer query heads a kv head, 16 head columns of a 16x16 MFMA are mostly
 // padding, and so is the softmax work done on them.  This pass 1 computes Q K^T on
 // v_mfma_f32_4x4x4_16b_f16 instead: 16 blocks of 4 keys x 4 heads, so a 64-key tile
@@ -666,6 +666,12 @@ __global__ __launch_bounds__(256) void qkv_pass1_q8_lds(DecodeParams p) {
 // pass 1 went 102.6 -> 102.3 us and C3 90 -> 89.5 us with the split.  K rows are stored with 16-byte chunk c at slot
 // c ^ hk(key) and V rows at c ^ hv(key), so the 128-bit K reads and the 32-bit V reads
 // are free of bank conflicts.
+// Two head groups (HG = 2, 5 <= G <= 8): the K fragments of a tile feed a second set of
+// 4x4x4 products against heads 4..7 (the fp16 form of the codes is shared), each group
+// keeps its own softmax state, and the P V A operand carries group 0 in rows 0..3 and
+// group 1 in rows 4..7 (row_take2), so P V costs no more MFMA than with one group.  The
+// 8 heads' q staging raises LDS to 21.5 KB a wave (16-bit q): 7 waves a CU instead of 8.
+// Flint's G = 8 over C2's rows: pass 1 74.7 us (16x16 register-fed kernel) -> 62.9 us.
 constexpr int kQT = 64;                     // keys a tile
 constexpr int kQSlot = 8192 + 8192 + 1024;  // K codes, V codes, ks / kb / vs / vb words
 
@@ -682,6 +688,20 @@ template <int SH>
 __device__ __forceinline__ uint32_t row_take(uint32_t x) {
   if constexpr (SH == 0) return x;
   else return uint32_t(__builtin_amdgcn_update_dpp(0, int(x), 0x100 + SH, 0xf, 0xf, true));
+}
+
+// Two head groups in one P V A operand: lanes 0..3 of each 16-lane row take x0 of lane i + 4 SG, lanes 4..7 take
+// x1 of lane i + 4 SG - 4 (lanes 8..15 are don't-care).  DPP bank_mask (4-lane banks) writes only one bank over
+// an `old` that already holds the other.
+template <int SG>
+__device__ __forceinline__ uint32_t row_take2(uint32_t x0, uint32_t x1) {
+  if constexpr (SG == 0)  // bank 1 <- x1 of lane i - 4 (row_shr:4) over x0
+    return uint32_t(__builtin_amdgcn_update_dpp(int(x0), int(x1), 0x114, 0xf, 0x2, false));
+  else if constexpr (SG == 1)  // bank 0 <- x0 of lane i + 4 (row_shl:4) over x1
+    return uint32_t(__builtin_amdgcn_update_dpp(int(x1), int(x0), 0x104, 0xf, 0x1, false));
+  else  // bank 0 <- x0 of lane i + 4 SG over x1 of lane i + 4 SG - 4
+    return uint32_t(__builtin_amdgcn_update_dpp(int(row_take<4 * SG - 4>(x1)), int(x0), 0x100 + 4 * SG, 0xf, 0x1,
+                                                false));
 }
 
 // Stream-K split of the quad pass 1: the (row, kv head, 64-key tile) list in row-major order
@@ -775,6 +795,26 @@ struct QStream {
   int r, kvh, t0, lo, hi, cnt;
   long long Gs;  // global index of its first tile
 };
+
+// Values equal in every lane, marked so for the compiler: what comes through a shuffle counts as divergent, and
+// buffer descriptors built from divergent values get a loop over their distinct values around every load.
+__device__ __forceinline__ int uni(int x) { return __builtin_amdgcn_readfirstlane(x); }
+__device__ __forceinline__ long long uni(long long x) {
+  const uint32_t lo = uint32_t(__builtin_amdgcn_readfirstlane(int(uint32_t(x))));
+  const uint32_t hi = uint32_t(__builtin_amdgcn_readfirstlane(int(uint32_t(uint64_t(x) >> 32))));
+  return (long long)((uint64_t(hi) << 32) | lo);
+}
+__device__ __forceinline__ QStream uni(const QStream& S) {
+  QStream u;
+  u.r = uni(S.r);
+  u.kvh = uni(S.kvh);
+  u.t0 = uni(S.t0);
+  u.lo = uni(S.lo);
+  u.hi = uni(S.hi);
+  u.cnt = uni(S.cnt);
+  u.Gs = uni(S.Gs);
+  return u;
+}
 // its buffer descriptors (built where used, so only one stream's are live at a time)
 struct QRsrc {
   BufRsrc rk, rv, rks, rkb, rvs, rvb;
@@ -799,7 +839,7 @@ __device__ __forceinline__ BufRsrc quad_qrsrc(const DecodeParams& p, const QStre
                    uint32_t(p.G * kHD * QB));
 }
 
-template <int QDT, int SDT>
+template <int QDT, int SDT, int HG>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void qkv_pass1_q8_quad(DecodeParams p) {
   const int wv = blockIdx.x;
   const int lane = threadIdx.x;
@@ -811,7 +851,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void
   if (p.R <= 64) {
     const int c = quad_lane_count(p.start, p.nkeys, p.n, p.cap, p.R, lane);
     const int incl = wave_incl_scan(c);
-    T = (long long)__shfl(incl, 63) * p.KVH;
+    T = uni((long long)__shfl(incl, 63) * p.KVH);
     W = int(min((long long)p.qwaves, max(1LL, T / p.qmint)));
     if (wv >= W) return;
     g = wv * T / W;
@@ -819,28 +859,31 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void
     if (g >= gend) return;
     const long long lo_t = (long long)(incl - c) * p.KVH, hi_t = (long long)incl * p.KVH;
     const unsigned long long m = __ballot(c > 0 && g >= lo_t && g < hi_t);
-    r0 = __ffsll((long long)m) - 1;
-    row_first = (long long)__shfl(incl - c, r0) * p.KVH;
+    r0 = uni(__ffsll((long long)m) - 1);
+    row_first = uni((long long)__shfl(incl - c, r0) * p.KVH);
   } else {
     long long unused;
     quad_split(p.start, p.nkeys, p.n, p.cap, p.R, p.KVH, p.qwaves, p.qmint, T, W, -1, unused);
+    T = uni(T);
+    W = uni(W);
     if (wv >= W) return;
     g = wv * T / W;
     gend = (wv + 1) * T / W;
     if (g >= gend) return;
-    r0 = quad_locate(p.start, p.nkeys, p.n, p.cap, p.R, p.KVH, g, row_first);
+    r0 = uni(quad_locate(p.start, p.nkeys, p.n, p.cap, p.R, p.KVH, g, row_first));
+    row_first = uni(row_first);
   }
 
   const int n = lane & 3;  // QK: head column of this lane
   const int c16 = lane & 15, q4 = lane >> 4;
-  const int G = p.G;       // <= 4
+  const int G = p.G;       // <= 4 HG
 
   // the tile slot in two named halves, so that the next tile's K loads can be in flight while V is read here:
   // K codes (8 KB) + ks / kb words, V codes (8 KB) + vs / vb words
   __shared__ __attribute__((aligned(16))) uint8_t qK[kQSlot / 2];
   __shared__ __attribute__((aligned(16))) uint8_t qV[kQSlot / 2];
-  __shared__ __attribute__((aligned(16))) uint8_t qraw[4 * kHD * QB];  // the next stream's q as loaded
-  __shared__ __attribute__((aligned(16))) _Float16 qh[4 * kHD];          // this stream's q in fp16
+  __shared__ __attribute__((aligned(16))) uint8_t qraw[4 * HG * kHD * QB];  // the next stream's q as loaded
+  __shared__ __attribute__((aligned(16))) _Float16 qh[4 * HG * kHD];          // this stream's q in fp16
   constexpr int kWaitAll = (0xF << 8) | (0x7 << 4);        // s_waitcnt vmcnt(0)
   constexpr int kWaitTen = (0xF << 8) | (0x7 << 4) | 10;    // s_waitcnt vmcnt(10)
   constexpr int kWaitLds = (0x3 << 14) | (0x7 << 4) | 0xF;  // s_waitcnt lgkmcnt(0)
@@ -882,7 +925,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void
   auto issue_q = [&](const QStream& S) {
     const BufRsrc rq = quad_qrsrc<QB>(p, S);
 #pragma unroll
-    for (int j = 0; j < 2 * QB; j++) lds_load4(rq, qraw + 256 * j, uint32_t(256 * j + 4 * lane));
+    for (int j = 0; j < 2 * QB * HG; j++) lds_load4(rq, qraw + 256 * j, uint32_t(256 * j + 4 * lane));
   };
 
   // the stream (row r0, kv head) holding tile g
@@ -891,6 +934,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void
   cur.cnt = quad_row_tiles(p.start, p.nkeys, p.n, p.cap, r0, cur.t0, cur.lo, cur.hi);
   cur.kvh = int((g - row_first) / cur.cnt);
   cur.Gs = row_first + (long long)cur.kvh * cur.cnt;
+  cur = uni(cur);
   int k0 = int(g - cur.Gs);
   issue(quad_rsrc(p, cur), cur, k0);
   issue_q(cur);
@@ -908,28 +952,34 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void
         nxt.r = quad_next_row(p.start, p.nkeys, p.n, p.cap, p.R, cur.r);
         nxt.cnt = quad_row_tiles(p.start, p.nkeys, p.n, p.cap, nxt.r, nxt.t0, nxt.lo, nxt.hi);
       }
+      nxt = uni(nxt);
     }
     const QRsrc D = quad_rsrc(p, cur);
     const int lo = cur.lo, hi = cur.hi;
     const int head0 = cur.kvh * G;
 
     __builtin_amdgcn_s_waitcnt(kWaitAll);
-    float qs0 = 0.0f, qs1 = 0.0f;  // sums of head n's fp16 q over dims [0, 64) and [64, 128)
-    {
-      // lane l converts elements 8 l .. 8 l + 7 (head l / 16, group (l / 8) & 1) into qh
+    const float C = p.scale_log2;
+    // per head group e (heads 4 e .. 4 e + 3): sums of head 4 e + n's fp16 q over dims [0, 64) and [64, 128),
+    // scaled
+    float zc0[HG], zc1[HG], qc0[HG], qc1[HG];
+#pragma unroll
+    for (int e = 0; e < HG; e++) {
+      // lane l converts elements 8 l .. 8 l + 7 of the group (head 4 e + l / 16, dim group (l / 8) & 1) into qh
       _Float16 t[8];
       float part = 0.0f;
 #pragma unroll
       for (int i = 0; i < 8; i++) {
-        t[i] = _Float16(ld16<QDT>(qraw, size_t(8 * lane + i)));
+        t[i] = _Float16(ld16<QDT>(qraw, size_t(4 * kHD * e + 8 * lane + i)));
         part += float(t[i]);
       }
 #pragma unroll
-      for (int i = 0; i < 8; i++) qh[8 * lane + i] = t[i];
+      for (int i = 0; i < 8; i++) qh[4 * kHD * e + 8 * lane + i] = t[i];
       part += __shfl_xor(part, 1);
       part += __shfl_xor(part, 2);
       part += __shfl_xor(part, 4);
-      // lane 16 h + 8 g holds the sum of head h, group g
+      // lane 16 h + 8 g holds the sum of head 4 e + h, dim group g
+      float qs0 = 0.0f, qs1 = 0.0f;
 #pragma unroll
       for (int h = 0; h < 4; h++) {
         const float g0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(part), 16 * h));
@@ -937,11 +987,19 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void
         qs0 = n == h ? g0 : qs0;
         qs1 = n == h ? g1 : qs1;
       }
+      zc0[e] = 1024.0f * qs0 * C;
+      zc1[e] = 1024.0f * qs1 * C;
+      qc0[e] = qs0 * C;
+      qc1[e] = qs1 * C;
     }
-    const float C = p.scale_log2;
-    const float zc0 = 1024.0f * qs0 * C, zc1 = 1024.0f * qs1 * C, qc0 = qs0 * C, qc1 = qs1 * C;
 
-    float m_run = -INFINITY, l_acc = 0.0f, wb0 = 0.0f, wb1 = 0.0f;
+    // softmax state of head 4 e + n
+    float m_run[HG], l_acc[HG], wb0[HG], wb1[HG];
+#pragma unroll
+    for (int e = 0; e < HG; e++) {
+      m_run[e] = -INFINITY;
+      l_acc[e] = wb0[e] = wb1[e] = 0.0f;
+    }
     f4 O[8];
 #pragma unroll
     for (int ii = 0; ii < 8; ii++) O[ii] = f4{0.0f, 0.0f, 0.0f, 0.0f};
@@ -974,91 +1032,130 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void
     };
 
     auto compute = [&](int kt, const QuadTile& T) {
-      // ---- S^T = K Q^T, four chains (group g = chunk >> 2, chunk parity)
-      f4 acc[4];
+      // ---- S^T = K Q^T for each head group, four chains each (dim group = chunk >> 2, chunk parity); the
+      // K codes' fp16 form is shared by the groups
+      f4 acc[HG][4];
   #pragma unroll
-      for (int i = 0; i < 4; i++) acc[i] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+      for (int e = 0; e < HG; e++)
+  #pragma unroll
+        for (int i = 0; i < 4; i++) acc[e][i] = f4{0.0f, 0.0f, 0.0f, 0.0f};
   #pragma unroll
       for (int cc = 0; cc < 8; cc++) {
         const u4 kv = T.k[cc];
-        const u4 qa = *reinterpret_cast<const u4*>(qh + kHD * n + 16 * cc);
-        const u4 qc = *reinterpret_cast<const u4*>(qh + kHD * n + 16 * cc + 8);
-        f4& a = acc[2 * (cc >> 2) + (cc & 1)];
-        a = mfma4(codes4_to_h4(kv.x), pack_h4(qa.x, qa.y), a);
-        a = mfma4(codes4_to_h4(kv.y), pack_h4(qa.z, qa.w), a);
-        a = mfma4(codes4_to_h4(kv.z), pack_h4(qc.x, qc.y), a);
-        a = mfma4(codes4_to_h4(kv.w), pack_h4(qc.z, qc.w), a);
+        const h4 kx = codes4_to_h4(kv.x), ky = codes4_to_h4(kv.y), kz = codes4_to_h4(kv.z), kw = codes4_to_h4(kv.w);
+  #pragma unroll
+        for (int e = 0; e < HG; e++) {
+          const u4 qa = *reinterpret_cast<const u4*>(qh + kHD * (4 * e + n) + 16 * cc);
+          const u4 qc = *reinterpret_cast<const u4*>(qh + kHD * (4 * e + n) + 16 * cc + 8);
+          f4& a = acc[e][2 * (cc >> 2) + (cc & 1)];
+          a = mfma4(kx, pack_h4(qa.x, qa.y), a);
+          a = mfma4(ky, pack_h4(qa.z, qa.w), a);
+          a = mfma4(kz, pack_h4(qc.x, qc.y), a);
+          a = mfma4(kw, pack_h4(qc.z, qc.w), a);
+        }
       }
       const uint32_t kscw[4] = {T.ksc.x, T.ksc.y, T.ksc.z, T.ksc.w}, kbiw[4] = {T.kbi.x, T.kbi.y, T.kbi.z, T.kbi.w};
       const uint32_t vscw[4] = {T.vsc.x, T.vsc.y, T.vsc.z, T.vsc.w}, vbiw[4] = {T.vbi.x, T.vbi.y, T.vbi.z, T.vbi.w};
-      // ---- scores of keys ts0 + m for head n (base-2 logits)
+      // ---- scores of keys ts0 + m for head 4 e + n (base-2 logits)
       const bool full = kt >= lo && kt + kQT <= hi;
-      float s[4];
+      float s[HG][4];
       bool valid[4];
   #pragma unroll
       for (int m = 0; m < 4; m++) {
-        const float a0 = acc[0][m] + acc[1][m], a1 = acc[2][m] + acc[3][m];
-        const float u0 = __builtin_fmaf(a0, C, -zc0), u1 = __builtin_fmaf(a1, C, -zc1);
-        float v = hpart<SDT>(kscw[m], 0) * u0;
-        v = __builtin_fmaf(hpart<SDT>(kscw[m], 1), u1, v);
-        v = __builtin_fmaf(hpart<SDT>(kbiw[m], 0), qc0, v);
-        v = __builtin_fmaf(hpart<SDT>(kbiw[m], 1), qc1, v);
         const int t = kt + ts0 + m;
         valid[m] = full || (t >= lo && t < hi);
-        s[m] = valid[m] ? v : -INFINITY;
+  #pragma unroll
+        for (int e = 0; e < HG; e++) {
+          const float a0 = acc[e][0][m] + acc[e][1][m], a1 = acc[e][2][m] + acc[e][3][m];
+          const float u0 = __builtin_fmaf(a0, C, -zc0[e]), u1 = __builtin_fmaf(a1, C, -zc1[e]);
+          float v = hpart<SDT>(kscw[m], 0) * u0;
+          v = __builtin_fmaf(hpart<SDT>(kscw[m], 1), u1, v);
+          v = __builtin_fmaf(hpart<SDT>(kbiw[m], 0), qc0[e], v);
+          v = __builtin_fmaf(hpart<SDT>(kbiw[m], 1), qc1[e], v);
+          s[e][m] = valid[m] ? v : -INFINITY;
+        }
       }
-      // ---- tile max of head n over the 16 lanes holding it
-      float tmax = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
-      tmax = fmaxf(tmax, __shfl_xor(tmax, 4));
-      tmax = fmaxf(tmax, __shfl_xor(tmax, 8));
-      tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
-      tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
-      const bool need = tmax > m_run + kRescaleThr;
-      if (__any(need)) {
-        const float corr = need ? (m_run == -INFINITY ? 0.0f : fast_exp2(m_run - tmax)) : 1.0f;
-        if (need) m_run = tmax;
-        l_acc *= corr;
-        wb0 *= corr;
-        wb1 *= corr;
-        // P V rows: lane (c16, q4) register i is head 4 q4 + i; heads 0..3 live in lanes 0..15
+      // ---- tile max of head 4 e + n over the 16 lanes holding it
+      float tmax[HG];
+      bool need[HG], any_need = false;
+  #pragma unroll
+      for (int e = 0; e < HG; e++) {
+        float x = fmaxf(fmaxf(s[e][0], s[e][1]), fmaxf(s[e][2], s[e][3]));
+        x = fmaxf(x, __shfl_xor(x, 4));
+        x = fmaxf(x, __shfl_xor(x, 8));
+        x = fmaxf(x, __shfl_xor(x, 16));
+        x = fmaxf(x, __shfl_xor(x, 32));
+        tmax[e] = x;
+        need[e] = x > m_run[e] + kRescaleThr;
+        any_need = any_need || need[e];
+      }
+      if (__any(any_need)) {
+        float corr[HG];
+  #pragma unroll
+        for (int e = 0; e < HG; e++) {
+          corr[e] = need[e] ? (m_run[e] == -INFINITY ? 0.0f : fast_exp2(m_run[e] - tmax[e])) : 1.0f;
+          if (need[e]) m_run[e] = tmax[e];
+          l_acc[e] *= corr[e];
+          wb0[e] *= corr[e];
+          wb1[e] *= corr[e];
+        }
+        // P V rows: lane (c16, q4) register i is head 4 q4 + i; head group e lives in lanes 16 e .. 16 e + 15
   #pragma unroll
         for (int i = 0; i < 4; i++) {
-          const float ci = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(corr), i));
+          float ci = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(corr[0]), i));
+          if constexpr (HG == 2) {
+            const float c1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(corr[HG - 1]), i));
+            ci = q4 == 1 ? c1 : ci;
+          }
   #pragma unroll
           for (int ii = 0; ii < 8; ii++) O[ii][i] *= ci;
         }
       }
-      float w0[4], w1[4];
+      // [e][g][pair]: fp16 hi / lo of w_g of head group e for keys m = 0, 1 and 2, 3
+      uint32_t wh[HG][4], wl[HG][4];
   #pragma unroll
-      for (int m = 0; m < 4; m++) {
-        float pr = fast_exp2(s[m] - m_run);
-        float x0 = pr * hpart<SDT>(vscw[m], 0), x1 = pr * hpart<SDT>(vscw[m], 1);
-        float y0 = pr * hpart<SDT>(vbiw[m], 0), y1 = pr * hpart<SDT>(vbiw[m], 1);
-        // garbage scales of keys outside the range must not reach the sums (0 * inf)
-        pr = valid[m] ? pr : 0.0f;
-        x0 = valid[m] ? x0 : 0.0f;
-        x1 = valid[m] ? x1 : 0.0f;
-        y0 = valid[m] ? y0 : 0.0f;
-        y1 = valid[m] ? y1 : 0.0f;
-        l_acc += pr;
-        w0[m] = x0;
-        w1[m] = x1;
-        wb0 += __builtin_fmaf(-1024.0f, x0, y0);
-        wb1 += __builtin_fmaf(-1024.0f, x1, y1);
+      for (int e = 0; e < HG; e++) {
+        float w0[4], w1[4];
+  #pragma unroll
+        for (int m = 0; m < 4; m++) {
+          float pr = fast_exp2(s[e][m] - m_run[e]);
+          float x0 = pr * hpart<SDT>(vscw[m], 0), x1 = pr * hpart<SDT>(vscw[m], 1);
+          float y0 = pr * hpart<SDT>(vbiw[m], 0), y1 = pr * hpart<SDT>(vbiw[m], 1);
+          // garbage scales of keys outside the range must not reach the sums (0 * inf)
+          pr = valid[m] ? pr : 0.0f;
+          x0 = valid[m] ? x0 : 0.0f;
+          x1 = valid[m] ? x1 : 0.0f;
+          y0 = valid[m] ? y0 : 0.0f;
+          y1 = valid[m] ? y1 : 0.0f;
+          l_acc[e] += pr;
+          w0[m] = x0;
+          w1[m] = x1;
+          wb0[e] += __builtin_fmaf(-1024.0f, x0, y0);
+          wb1[e] += __builtin_fmaf(-1024.0f, x1, y1);
+        }
+        split_h2(w0[0], w0[1], wh[e][0], wl[e][0]);
+        split_h2(w0[2], w0[3], wh[e][1], wl[e][1]);
+        split_h2(w1[0], w1[1], wh[e][2], wl[e][2]);
+        split_h2(w1[2], w1[3], wh[e][3], wl[e][3]);
       }
-      uint32_t wh[4], wl[4];  // [g][pair]: fp16 hi / lo of w_g for keys m = 0, 1 and 2, 3
-      split_h2(w0[0], w0[1], wh[0], wl[0]);
-      split_h2(w0[2], w0[3], wh[1], wl[1]);
-      split_h2(w1[0], w1[1], wh[2], wl[2]);
-      split_h2(w1[2], w1[3], wh[3], wl[3]);
 
-      // ---- P V on 16x16x16, one 16-key sub-tile at a time
+      // ---- P V on 16x16x16, one 16-key sub-tile at a time.  A row c16 < 4 (head c16) takes group 0's w of
+      // lane c16 + 4 sigma; with two groups, row 4 + j (head 4 + j) takes group 1's w of lane j + 4 sigma
+      auto take = [&](auto sig, uint32_t x0, uint32_t x1) -> uint32_t {
+        constexpr int SG = decltype(sig)::value;
+        if constexpr (HG == 1) {
+          (void)x1;
+          return row_take<4 * SG>(x0);
+        } else {
+          return row_take2<SG>(x0, x1);
+        }
+      };
       auto pv = [&](auto sig) {
         constexpr int SG = decltype(sig)::value;
-        const h4 A0h = pack_h4(row_take<4 * SG>(wh[0]), row_take<4 * SG>(wh[1]));
-        const h4 A0l = pack_h4(row_take<4 * SG>(wl[0]), row_take<4 * SG>(wl[1]));
-        const h4 A1h = pack_h4(row_take<4 * SG>(wh[2]), row_take<4 * SG>(wh[3]));
-        const h4 A1l = pack_h4(row_take<4 * SG>(wl[2]), row_take<4 * SG>(wl[3]));
+        const h4 A0h = pack_h4(take(sig, wh[0][0], wh[HG - 1][0]), take(sig, wh[0][1], wh[HG - 1][1]));
+        const h4 A0l = pack_h4(take(sig, wl[0][0], wl[HG - 1][0]), take(sig, wl[0][1], wl[HG - 1][1]));
+        const h4 A1h = pack_h4(take(sig, wh[0][2], wh[HG - 1][2]), take(sig, wh[0][3], wh[HG - 1][3]));
+        const h4 A1l = pack_h4(take(sig, wl[0][2], wl[HG - 1][2]), take(sig, wl[0][3], wl[HG - 1][3]));
         const uint32_t (&vd)[8] = T.v[SG];
         h4 bv[8];
   #pragma unroll
@@ -1114,32 +1211,46 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void
     }
 
     // ---- this segment's partial: heads 0..G-1 of the kv head, slot j of the stream
-    l_acc += __shfl_xor(l_acc, 4);
-    l_acc += __shfl_xor(l_acc, 8);
-    l_acc += __shfl_xor(l_acc, 16);
-    l_acc += __shfl_xor(l_acc, 32);
-    wb0 += __shfl_xor(wb0, 4);
-    wb0 += __shfl_xor(wb0, 8);
-    wb0 += __shfl_xor(wb0, 16);
-    wb0 += __shfl_xor(wb0, 32);
-    wb1 += __shfl_xor(wb1, 4);
-    wb1 += __shfl_xor(wb1, 8);
-    wb1 += __shfl_xor(wb1, 16);
-    wb1 += __shfl_xor(wb1, 32);
+#pragma unroll
+    for (int e = 0; e < HG; e++) {
+      l_acc[e] += __shfl_xor(l_acc[e], 4);
+      l_acc[e] += __shfl_xor(l_acc[e], 8);
+      l_acc[e] += __shfl_xor(l_acc[e], 16);
+      l_acc[e] += __shfl_xor(l_acc[e], 32);
+      wb0[e] += __shfl_xor(wb0[e], 4);
+      wb0[e] += __shfl_xor(wb0[e], 8);
+      wb0[e] += __shfl_xor(wb0[e], 16);
+      wb0[e] += __shfl_xor(wb0[e], 32);
+      wb1[e] += __shfl_xor(wb1[e], 4);
+      wb1[e] += __shfl_xor(wb1[e], 8);
+      wb1[e] += __shfl_xor(wb1[e], 16);
+      wb1[e] += __shfl_xor(wb1[e], 32);
+    }
     const int jslot = wv - quad_wave_of(cur.Gs, T, W);
-    if (q4 == 0) {
+    // lanes of quad q4 < HG write head group q4: row i of O is head 4 q4 + i
+    if (q4 < HG) {
+      const int e = HG == 1 ? 0 : q4;
+      const float mr = HG == 1 ? m_run[0] : (e ? m_run[HG - 1] : m_run[0]);
+      const float la = HG == 1 ? l_acc[0] : (e ? l_acc[HG - 1] : l_acc[0]);
 #pragma unroll
       for (int i = 0; i < 4; i++) {
-        if (i < G) {
-          const float b0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wb0), i));
-          const float b1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wb1), i));
-          const size_t part = (size_t(cur.r) * p.H + head0 + i) * p.nchunks + jslot;
+        float b0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wb0[0]), i));
+        float b1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wb1[0]), i));
+        if constexpr (HG == 2) {
+          const float c0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wb0[HG - 1]), i));
+          const float c1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wb1[HG - 1]), i));
+          b0 = e ? c0 : b0;
+          b1 = e ? c1 : b1;
+        }
+        const int h = 4 * e + i;
+        if (h < G) {
+          const size_t part = (size_t(cur.r) * p.H + head0 + h) * p.nchunks + jslot;
           float4* po = reinterpret_cast<float4*>(p.po + part * kHD);
           po[c16] = make_float4(O[0][i] + b0, O[1][i] + b0, O[2][i] + b0, O[3][i] + b0);
           po[16 + c16] = make_float4(O[4][i] + b1, O[5][i] + b1, O[6][i] + b1, O[7][i] + b1);
           if (c16 == i) {
-            p.pm[part] = m_run;
-            p.pl[part] = l_acc;
+            p.pm[part] = mr;
+            p.pl[part] = la;
           }
         }
       }
@@ -1430,7 +1541,8 @@ __global__ __launch_bounds__(256) void decode_combine(CombineParams p) {
 
 using namespace lcl;
 
-// 8-bit pass 1 variant: the quad kernel for G <= 4, the register-fed one otherwise.  LOCALS_AMD_DECODE=reg
+// 8-bit pass 1 variant: the quad kernel for G <= 8 (one head group for G <= 4, two above), the register-fed one
+// otherwise.  LOCALS_AMD_DECODE=reg
 // or =lds forces the register-fed or the LDS-staged 16x16 kernel (for comparisons).
 enum { kVarAuto = 0, kVarReg = 1, kVarLds = 2 };
 static int decode_variant() {
@@ -1442,12 +1554,14 @@ static int decode_variant() {
   return v;
 }
 
-static bool use_quad(const DecodeParams& p) { return p.G <= 4 && decode_variant() == kVarAuto; }
+static bool use_quad(const DecodeParams& p) { return p.G <= 8 && decode_variant() == kVarAuto; }
 
 template <int QDT, int SDT>
 static void launch_q8_t(dim3 grid, hipStream_t stream, hipEvent_t e0, hipEvent_t e1, const DecodeParams& p) {
-  if (use_quad(p))
-    hipExtLaunchKernelGGL((qkv_pass1_q8_quad<QDT, SDT>), grid, dim3(64), 0, stream, e0, e1, 0, p);
+  if (use_quad(p) && p.G <= 4)
+    hipExtLaunchKernelGGL((qkv_pass1_q8_quad<QDT, SDT, 1>), grid, dim3(64), 0, stream, e0, e1, 0, p);
+  else if (use_quad(p))
+    hipExtLaunchKernelGGL((qkv_pass1_q8_quad<QDT, SDT, 2>), grid, dim3(64), 0, stream, e0, e1, 0, p);
   else if (decode_variant() == kVarLds)
     hipExtLaunchKernelGGL((qkv_pass1_q8_lds<QDT, SDT>), grid, dim3(256), 0, stream, e0, e1, 0, p);
   else hipExtLaunchKernelGGL((qkv_pass1_q8<QDT, SDT>), grid, dim3(256), 0, stream, e0, e1, 0, p);
@@ -1515,20 +1629,40 @@ static int quad_slots(int extent, int chunk) {
   const int tiles = (max(extent, 1) + kQT - 1) / kQT;
   return (tiles + quad_mint(chunk) - 1) / quad_mint(chunk) + 1;
 }
-// waves of the quad pass 1: two a SIMD (the kernel's occupancy), one resident round
-static int quad_waves() {
-  static int cache[64] = {0};
+// resident waves a CU of the two-head-group quad pass 1 (its 8 heads' q staging leaves room for 7 a CU with
+// 16-bit q, 6 with fp32 q); 6 if the runtime cannot tell
+template <int QDT, int SDT>
+static int quad_hg2_per_cu() {
+  int nb = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, qkv_pass1_q8_quad<QDT, SDT, 2>, 64, 0) != hipSuccess ||
+      nb <= 0)
+    nb = 6;
+  return min(nb, 8);
+}
+static int quad_hg2_per_cu(int qdt, int sdt) {
+  if (sdt == DT_BF16)
+    return qdt == DT_F16 ? quad_hg2_per_cu<DT_F16, DT_BF16>() : qdt == DT_BF16 ? quad_hg2_per_cu<DT_BF16, DT_BF16>()
+                                                                              : quad_hg2_per_cu<DT_F32, DT_BF16>();
+  return qdt == DT_F16 ? quad_hg2_per_cu<DT_F16, DT_F16>() : qdt == DT_BF16 ? quad_hg2_per_cu<DT_BF16, DT_F16>()
+                                                                           : quad_hg2_per_cu<DT_F32, DT_F16>();
+}
+
+// waves of the quad pass 1, one resident round: two a SIMD for G <= 4 (the kernel's occupancy), the occupancy
+// calculator's count for 5 <= G <= 8
+static int quad_waves(int G, int qdt, int sdt) {
+  static int cache[64][7] = {{0}};  // [device][0: G <= 4, 1 + 2 qdt + sdt: the two-group kernel]
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
-  if (!cache[dev]) {
+  const int v = G <= 4 ? 0 : 1 + 2 * qdt + sdt;
+  if (!cache[dev][v]) {
     int cus = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
-    cache[dev] = 2 * 4 * cus;
+    cache[dev][v] = (v == 0 ? 2 * 4 : quad_hg2_per_cu(qdt, sdt)) * cus;
     // LOCALS_AMD_DECODE_WAVES overrides the count (a tuning knob: fewer waves than resident slots)
     const char* e = getenv("LOCALS_AMD_DECODE_WAVES");
-    if (e && atoi(e) > 0) cache[dev] = atoi(e);
+    if (e && atoi(e) > 0) cache[dev][v] = atoi(e);
   }
-  return cache[dev];
+  return cache[dev][v];
 }
 
 extern "C" {
@@ -1581,7 +1715,7 @@ int lcl_qkv_attend_ex(const void* q, int qdt, const uint32_t* kw, const void* ks
   if (quad) {
     p.qmint = quad_mint(chunk);
     const long long tmax = (long long)B * KVH * ((n + kQT - 1) / kQT);
-    p.qwaves = int(min((long long)quad_waves(), max(1LL, tmax / p.qmint)));
+    p.qwaves = int(min((long long)quad_waves(p.G, qdt, sdt), max(1LL, tmax / p.qmint)));
   }
   if (n > 0) {
     const dim3 grid = quad ? dim3(p.qwaves) : dim3(nparts, KVH * p.nslices, B);

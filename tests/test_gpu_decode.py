@@ -2,7 +2,8 @@
 
 Cases follow the reference's own test (tests/test_flint.py:278-295: (B, n, cap, pads) =
 (1,1,256,[0]), (1,13,256,[0]), (1,2100,2304,[0]), (3,700,768,[0,37,300]), K ~ 2 N(0,1), sinks ~ 2 N(0,1), scale
-0.0884) over the head layouts (32,4) and (4,2) it uses plus the BASELINE shapes (32/8, 16/8) and G = 1, 6, 16, 32.
+0.0884) over the head layouts (32,4) and (4,2) it uses plus the BASELINE shapes (32/8, 16/8) and G = 1, 5, 6, 7, 16, 32
+(G <= 4 takes the one-head-group quad pass 1, 5 <= G <= 8 the two-group one, larger G the register-fed kernel).
 Bar: max |got - oracle| <= 2e-3 for fp16 outputs; bf16 uses the reference's 2^-7 (1 + max|ref|).
 """
 
@@ -16,7 +17,7 @@ from tests.inputs import normal16, q8_cache, rng, to_torch, triple_to_torch
 pytestmark = pytest.mark.gpu
 
 CASES = [(1, 1, 256, [0]), (1, 13, 256, [0]), (1, 2100, 2304, [0]), (3, 700, 768, [0, 37, 300])]
-HEADS = [(32, 4), (24, 4), (4, 2), (32, 8), (16, 8), (8, 8), (16, 1), (32, 1)]
+HEADS = [(32, 4), (24, 4), (20, 4), (28, 4), (4, 2), (32, 8), (16, 8), (8, 8), (16, 1), (32, 1)]
 
 
 def _out(t):
@@ -132,6 +133,27 @@ def test_attend_bf16(dev):
     assert np.abs(_out(got) - ref).max() <= 2 ** -7 * (1 + np.abs(ref).max())
 
 
+@pytest.mark.parametrize("H,KVH", [(32, 8), (32, 4), (32, 1)])
+def test_attend_fp32_query(dev, H, KVH):
+    """fp32 queries (staged at 4 bytes a dim by the quad pass 1), fp16-representable so the oracle's fp16 q is the
+    same query; the output is fp32."""
+    from locals_amd import qkv
+
+    g = rng(15 + H + KVH)
+    B, cap, n = 3, 768, 700
+    q = normal16(g, (B, H, 1, 128))
+    K, V = q8_cache(g, B, KVH, cap, kscale=2.0)
+    sinks = normal16(g, (H,), 2.0)
+    start = np.array([0, 37, 300], dtype=np.int32)
+    qt = to_torch(q, dev).float()
+    got = qkv.attend(qt, triple_to_torch(K, dev), triple_to_torch(V, dev), n, to_torch(sinks, dev), 0.0884,
+                     to_torch(start, dev))
+    torch.cuda.synchronize()
+    assert got.dtype == torch.float32
+    ref = oattn.attend(q, K, V, n, sinks, 0.0884, start)
+    assert np.abs(_out(got) - ref).max() <= 2e-3
+
+
 @pytest.mark.parametrize("H,Hkv", [(16, 8), (8, 8), (32, 4)])
 @pytest.mark.parametrize("kvdt", ["float16", "bfloat16"])
 def test_ragged_matches_oracle(dev, H, Hkv, kvdt):
@@ -156,13 +178,14 @@ def test_ragged_matches_oracle(dev, H, Hkv, kvdt):
     assert (_out(got)[2] == 0).all()
 
 
-def test_attend_many_rows(dev):
+@pytest.mark.parametrize("H,KVH", [(8, 2), (24, 4)])
+def test_attend_many_rows(dev, H, KVH):
     """More than 64 rows (the quad pass 1 then scans the rows 64 at a time to split its work) with ragged left
     padding, empty rows and a row whose keys start mid-tile."""
     from locals_amd import qkv
 
-    g = rng(14)
-    B, H, KVH, cap, n = 100, 8, 2, 640, 600
+    g = rng(14 + H)
+    B, cap, n = 100, 640, 600
     q = normal16(g, (B, H, 1, 128))
     K, V = q8_cache(g, B, KVH, cap, kscale=2.0)
     sinks = normal16(g, (H,), 2.0)
