@@ -34,12 +34,13 @@ def _replays(dev, graph_fn, eager_fn, refill, n=3):
             assert torch.equal(a, b), i
 
 
-def test_decode_step_replays(dev):
-    """qkv.attend over a left-padded batch (stream-K pass 1 + combine)."""
+@pytest.mark.parametrize("H,KVH", [(32, 8), (32, 4)])
+def test_decode_step_replays(dev, H, KVH):
+    """qkv.attend over a left-padded batch (stream-K pass 1 + combine; one and two head groups)."""
     from locals_amd import qkv
 
-    g = rng(50)
-    B, H, KVH, cap, n = 4, 32, 8, 1024, 1000
+    g = rng(50 + KVH)
+    B, cap, n = 4, 1024, 1000
     K, V = q8_cache(g, B, KVH, cap)
     Kt, Vt = triple_to_torch(K, dev), triple_to_torch(V, dev)
     q = to_torch(normal16(g, (B, H, 1, 128)), dev)
