@@ -121,7 +121,8 @@ struct RawTile {
 // Direct buffer -> LDS loads issued as asm, outside the compiler's LDS-DMA wait tracking (merged at a loop head it
 // cannot tell two slots apart and makes every read of one wait for the loads into the other).  Their completion
 // is awaited with explicit s_waitcnt vmcnt by the caller, before a barrier.  Lane l's 16 bytes at voff land at
-// lds + 16 l; the descriptor covers `bytes` bytes (loads past it read 0), raw, non-temporal.
+// lds + 16 l; the descriptor covers `bytes` bytes (loads past it read 0), raw, default cache policy (every row
+// block of a kv head reads the same K/V, so the lines are worth keeping in L2).
 typedef uint32_t sg4 __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ sg4 rsrc_words(const void* p, uint32_t bytes) {
   const uint64_t a = reinterpret_cast<uint64_t>(p);
@@ -131,7 +132,7 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return uint32_t(uintptr_t((const __attribute__((address_space(3))) uint8_t*)(p)));
 }
 __device__ __forceinline__ void dma16(sg4 r, uint32_t lds, uint32_t voff) {
-  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen nt lds" : : "s"(lds), "v"(voff), "s"(r)
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" : : "s"(lds), "v"(voff), "s"(r)
                : "memory", "m0");
 }
 
@@ -275,10 +276,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     for (int i = 0; i < 2; i++) {
       const int r = 16 * wave + 8 * i + (lane >> 3);
       const uint32_t voff = uint32_t(t0 + r) * 128u + 16u * uint32_t((lane & 7) ^ ((r >> 1) & 1));
-      lds_load16(rk, S + 2048 * wave + 1024 * i, voff);
-      lds_load16(rv, S + 8192 + 2048 * wave + 1024 * i, voff);
+      lds_load16<0>(rk, S + 2048 * wave + 1024 * i, voff);
+      lds_load16<0>(rv, S + 8192 + 2048 * wave + 1024 * i, voff);
     }
-    lds_load4(rsw, S + 16384 + 256 * wave, (uint32_t(t0) + uint32_t(lane)) * 4u);
+    lds_load4<0>(rsw, S + 16384 + 256 * wave, (uint32_t(t0) + uint32_t(lane)) * 4u);
   };
   // the thread's share of a raw tile in LDS, as the register-prefetch path would hold it
   auto load_lds = [&](const uint8_t* S, RawTile& T) __attribute__((always_inline)) {
