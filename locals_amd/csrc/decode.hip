@@ -876,7 +876,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void
 
   const int n = lane & 3;  // QK: head column of this lane
   const int c16 = lane & 15, q4 = lane >> 4;
-  const int G = p.G;       // <= 4 HG
+  const int G = p.G;       // <= 4 * HG
 
   // the tile slot in two named halves, so that the next tile's K loads can be in flight while V is read here:
   // K codes (8 KB) + ks / kb words, V codes (8 KB) + vs / vb words
