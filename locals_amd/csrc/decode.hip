@@ -1531,10 +1531,7 @@ __global__ __launch_bounds__(256) void decode_combine(CombineParams p) {
   }
   const float inv = Lt > 0.0f ? 1.0f / Lt : 0.0f;
   const size_t ob = size_t(rh) * kHD + 4 * nd * ds + 4 * tid;
-  store_from_f32(p.out, ob + 0, t.x * inv, p.odt);
-  store_from_f32(p.out, ob + 1, t.y * inv, p.odt);
-  store_from_f32(p.out, ob + 2, t.z * inv, p.odt);
-  store_from_f32(p.out, ob + 3, t.w * inv, p.odt);
+  store4_from_f32(p.out, ob, t.x * inv, t.y * inv, t.z * inv, t.w * inv, p.odt);
 }
 
 }  // namespace lcl

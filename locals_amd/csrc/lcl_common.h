@@ -50,6 +50,35 @@ __device__ __forceinline__ void store_from_f32(void* p, size_t i, float v, int d
   else static_cast<float*>(p)[i] = v;
 }
 
+// elements i .. i + 3 of dtype dt: one 8-byte store (16-bit) or 16-byte store (fp32) where the address is aligned
+// for it, else four element stores; the same rounding as store_from_f32
+__device__ __forceinline__ void store4_from_f32(void* p, size_t i, float a, float b, float c, float d, int dt) {
+  if (dt == DT_F32) {
+    float* q = static_cast<float*>(p) + i;
+    if ((reinterpret_cast<uintptr_t>(q) & 15u) == 0) {
+      *reinterpret_cast<float4*>(q) = make_float4(a, b, c, d);
+      return;
+    }
+  } else {
+    uint16_t* q = static_cast<uint16_t*>(p) + i;
+    if ((reinterpret_cast<uintptr_t>(q) & 7u) == 0) {
+      uint16_t h[4];
+      if (dt == DT_BF16) {
+        h[0] = f32_to_bf16_bits(a); h[1] = f32_to_bf16_bits(b); h[2] = f32_to_bf16_bits(c); h[3] = f32_to_bf16_bits(d);
+      } else {
+        h[0] = __builtin_bit_cast(uint16_t, _Float16(a)); h[1] = __builtin_bit_cast(uint16_t, _Float16(b));
+        h[2] = __builtin_bit_cast(uint16_t, _Float16(c)); h[3] = __builtin_bit_cast(uint16_t, _Float16(d));
+      }
+      *reinterpret_cast<uint2*>(q) = make_uint2(h[0] | (uint32_t(h[1]) << 16), h[2] | (uint32_t(h[3]) << 16));
+      return;
+    }
+  }
+  store_from_f32(p, i + 0, a, dt);
+  store_from_f32(p, i + 1, b, dt);
+  store_from_f32(p, i + 2, c, dt);
+  store_from_f32(p, i + 3, d, dt);
+}
+
 // element k (0/1) of a packed pair of 16-bit values of dtype dt
 __device__ __forceinline__ float half_of(uint32_t w, int k, int dt) {
   const uint16_t b = uint16_t(k ? (w >> 16) : (w & 0xffffu));

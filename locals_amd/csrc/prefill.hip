@@ -194,8 +194,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       if (p.direct) {
 #pragma unroll
         for (int dd = 0; dd < 8; dd++)
-#pragma unroll
-          for (int i = 0; i < 4; i++) store_from_f32(p.out, row * kD + 16 * dd + 4 * q4 + i, 0.0f, p.odt);
+          store4_from_f32(p.out, row * kD + 16 * dd + 4 * q4, 0.0f, 0.0f, 0.0f, 0.0f, p.odt);
       } else if (q4 == 0) {
         p.pm[row * p.nchunks + c] = -INFINITY;
         p.pl[row * p.nchunks + c] = 0.0f;
@@ -598,8 +597,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       const float w = Lt > 0.0f ? f / Lt : 0.0f;
 #pragma unroll
       for (int dd = 0; dd < 8; dd++)
-#pragma unroll
-        for (int i = 0; i < 4; i++) store_from_f32(p.out, row * kD + 16 * dd + 4 * q4 + i, O[r][dd][i] * w, p.odt);
+        store4_from_f32(p.out, row * kD + 16 * dd + 4 * q4, O[r][dd][0] * w, O[r][dd][1] * w, O[r][dd][2] * w,
+                        O[r][dd][3] * w, p.odt);
       continue;
     }
     const size_t part = ((size_t(b) * p.H + head[r]) * p.L + qi[r]) * p.nchunks + c;
@@ -658,10 +657,7 @@ __global__ __launch_bounds__(256) void sdpa_combine(SdpaCombineParams p) {
   }
   const float w = Lt > 0.0f ? f / Lt : 0.0f;
   const size_t ob = size_t(row) * kD + 4 * lane;
-  store_from_f32(p.out, ob + 0, o.x * w, p.odt);
-  store_from_f32(p.out, ob + 1, o.y * w, p.odt);
-  store_from_f32(p.out, ob + 2, o.z * w, p.odt);
-  store_from_f32(p.out, ob + 3, o.w * w, p.odt);
+  store4_from_f32(p.out, ob, o.x * w, o.y * w, o.z * w, o.w * w, p.odt);
 }
 
 template <int QDT, int SDT, int FMT, int MT, int MASK>

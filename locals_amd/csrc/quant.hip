@@ -106,8 +106,8 @@ __global__ __launch_bounds__(256) void dequantize_rows(DequantParams p) {
   const uint32_t x = p.words[wid];
   const float s = load_as_f32(p.scales, row * (p.D / 64) + g, p.sdt);
   const float b = load_as_f32(p.biases, row * (p.D / 64) + g, p.sdt);
-#pragma unroll
-  for (int i = 0; i < 4; i++) store_from_f32(p.out, row * p.D + 4 * w + i, s * float((x >> (8 * i)) & 0xffu) + b, p.odt);
+  store4_from_f32(p.out, row * p.D + 4 * w, s * float(x & 0xffu) + b, s * float((x >> 8) & 0xffu) + b,
+                  s * float((x >> 16) & 0xffu) + b, s * float(x >> 24) + b, p.odt);
 }
 
 }  // namespace lcl
