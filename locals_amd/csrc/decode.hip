@@ -131,6 +131,14 @@ __device__ __forceinline__ float ld16(const void* p, size_t i) {
   else return f16_bits_to_f32(static_cast<const uint16_t*>(p)[i]);
 }
 
+// elements i .. i + N - 1 (N a multiple of 8) of dtype DT as fp32, loaded unconditionally (the compiler turns the
+// runs into 16-byte loads; gfx950 takes unaligned ones)
+template <int DT, int N>
+__device__ __forceinline__ void ldn(const void* p, size_t i, float (&v)[N]) {
+#pragma unroll
+  for (int j = 0; j < N; j++) v[j] = ld16<DT>(p, i + j);
+}
+
 template <int DT>
 __device__ __forceinline__ float hpart(uint32_t w, int k) {
   const uint16_t b = uint16_t(k ? (w >> 16) : (w & 0xffffu));
@@ -214,12 +222,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
   {
     const bool real = c16 < Gs;
     const size_t qrow = (size_t(r) * p.H + head0 + (real ? c16 : 0)) * kHD;
+    float qv0[16], qv1[16];  // dims 16 q4 .. + 15 and 64 + 16 q4 .. + 15 of the lane's head
+    ldn<QDT, 16>(p.q, qrow + 16 * q4, qv0);
+    ldn<QDT, 16>(p.q, qrow + 64 + 16 * q4, qv1);
 #pragma unroll
     for (int j = 0; j < 8; j++) {
       _Float16 t[4];
 #pragma unroll
       for (int i = 0; i < 4; i++) {
-        t[i] = _Float16(real ? ld16<QDT>(p.q, qrow + 64 * (j >> 2) + 16 * q4 + 4 * (j & 3) + i) : 0.0f);
+        t[i] = _Float16(real ? (j < 4 ? qv0[4 * j + i] : qv1[4 * (j - 4) + i]) : 0.0f);
         (j < 4 ? qs0 : qs1) += float(t[i]);
       }
       qb[j] = h4{t[0], t[1], t[2], t[3]};
@@ -456,12 +467,15 @@ __global__ __launch_bounds__(256) void qkv_pass1_q8_lds(DecodeParams p) {
   {
     const bool real = c16 < Gs;
     const size_t qrow = (size_t(r) * p.H + head0 + (real ? c16 : 0)) * kHD;
+    float qv0[16], qv1[16];  // dims 16 q4 .. + 15 and 64 + 16 q4 .. + 15 of the lane's head
+    ldn<QDT, 16>(p.q, qrow + 16 * q4, qv0);
+    ldn<QDT, 16>(p.q, qrow + 64 + 16 * q4, qv1);
 #pragma unroll
     for (int j = 0; j < 8; j++) {
       _Float16 t[4];
 #pragma unroll
       for (int i = 0; i < 4; i++) {
-        t[i] = _Float16(real ? ld16<QDT>(p.q, qrow + 64 * (j >> 2) + 16 * q4 + 4 * (j & 3) + i) : 0.0f);
+        t[i] = _Float16(real ? (j < 4 ? qv0[4 * j + i] : qv1[4 * (j - 4) + i]) : 0.0f);
         (j < 4 ? qs0 : qs1) += float(t[i]);
       }
       qb[j] = h4{t[0], t[1], t[2], t[3]};
@@ -1293,12 +1307,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
   {
     const bool real = c16 < Gs;
     const size_t qrow = (size_t(r) * p.H + head0 + (real ? c16 : 0)) * kHD;
+    float qv[32];  // dims 32 q4 .. 32 q4 + 31 of the lane's head
+    ldn<QDT, 32>(p.q, qrow + 32 * q4, qv);
 #pragma unroll
     for (int j = 0; j < 8; j++) {
       uint32_t bits[4];
 #pragma unroll
       for (int i = 0; i < 4; i++) {
-        const float v = real ? ld16<QDT>(p.q, qrow + 32 * q4 + 4 * j + i) : 0.0f;
+        const float v = real ? qv[4 * j + i] : 0.0f;
         bits[i] = KDT == DT_BF16 ? f32_to_bf16_bits(v) : __builtin_bit_cast(uint16_t, _Float16(v));
       }
       qb[j][0] = bits[0] | (bits[1] << 16);
