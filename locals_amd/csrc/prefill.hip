@@ -41,7 +41,10 @@ namespace lcl {
 
 constexpr int kD = 128;
 constexpr int kKT = 64;                 // keys a tile
-constexpr int kKsStride = 136;          // halves a K row in LDS (272 B: 16 B aligned, 4-bank skew a row)
+// halves a K row in LDS: 288 B, 16 B aligned with an 8-bank skew a row (measured on C4 / C5 against strides of 128,
+// 136, 152 and 160 halves and a 256 B row with the 16-bit path's XOR chunk swizzle: 136 -> 144 took C4 pass 1
+// 220.6 -> 216.5 us and C5 55.5 -> 53.0 us; no padding costs 30%)
+constexpr int kKsStride = 144;
 constexpr int kRawSlot = 8192 + 8192 + 1024;  // an 8-bit raw tile: K codes, V codes, ks / kb / vs / vb
 constexpr float kThr = 6.0f;
 // A 16-bit K + V tile (64 key rows of 256 B each).  Key row r keeps its 16-byte chunk c at slot c ^ sw16(r), a
