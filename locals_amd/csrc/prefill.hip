@@ -452,8 +452,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
           }
         }
       }
-      tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
-      tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+      tmax = max_x32(max_x16(tmax));
       if (tmax > m_run[r] + kThr) {  // lane-local rescale (O^T rows live in this lane column)
         const float corr = m_run[r] == -INFINITY ? 0.0f : fast_exp2(m_run[r] - tmax);
         m_run[r] = tmax;
@@ -585,8 +584,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
   for (int r = 0; r < RT; r++) {
     float l = l_acc[r];
-    l += __shfl_xor(l, 16);
-    l += __shfl_xor(l, 32);
+    l = add_x32(add_x16(l));
     if (!real[r]) continue;
     if (p.direct) {  // the only chunk: join with the sink here, as sdpa_combine would
       const size_t row = (size_t(b) * p.H + head[r]) * p.L + qi[r];
