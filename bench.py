@@ -458,17 +458,7 @@ def main():
     dev = torch.device("cuda:0")
     if args.calibrate_copy:
         n = args.calibrate_copy << 20
-        src = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
-        dst = torch.empty_like(src)
-        dst.copy_(src)
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        torch.cuda.synchronize()
-        e0.record()
-        for _ in range(args.steps):
-            dst.copy_(src)
-        e1.record()
-        torch.cuda.synchronize()
-        ms = e0.elapsed_time(e1) / args.steps
+        ms = copy_ms(n, args.steps, dev)
         print(json.dumps({"calibrate_copy_bytes": n, "dispatches": args.steps, "ms_per_copy": round(ms, 4),
                           "copy_GBs_read_plus_write": round(2 * n / ms / 1e6, 1)}), flush=True)
         return
@@ -531,6 +521,10 @@ def main():
     region_ms = ev.ms(2 * K_, 2 * K_ + 1)
     p1 = np.array([ev.ms(2 * i, 2 * i + 1) for i in range(0, K_, every)])
     ev.close()
+    # secondary rooflines, outside the timed region: what a plain 1 GiB device copy and a plain streaming read of
+    # 1 GiB move per second on this part
+    copy_gbs = 2 * (1 << 30) / copy_ms(1 << 30, 20, dev) / 1e6
+    read_gbs, read_how = read_probe(1 << 30, 20, dev)
 
     ms_step = region_ms / K_
     # the pass-1 kernel the library runs for this head ratio (4x4x4-MFMA stream-K kernel for G <= 8)
@@ -563,7 +557,10 @@ def main():
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "avg_us": round(p1_us, 2), "p10_us": round(float(np.percentile(p1, 10)) * 1e3, 2),
                      "p90_us": round(float(np.percentile(p1, 90)) * 1e3, 2), "bytes_per_launch": b_p1,
-                     "traffic": _traffic(cfg["name"], kernel)},
+                     "traffic": _traffic(cfg["name"], kernel),
+                     "measured_copy_GBs": round(copy_gbs, 1), "frac_of_measured_copy": round(achieved / copy_gbs, 4),
+                     "measured_read_GBs": round(read_gbs, 1), "measured_read_setting": read_how,
+                     "frac_of_measured_read": round(achieved / read_gbs, 4)},
         "cpu_baseline": None,
     }
     if cfg["name"] == "c4":
@@ -577,6 +574,73 @@ def main():
                                           f"C restatement of qkv.py's two passes (oracle/c/oracle.c), OpenMP",
                                 "max_abs_diff_vs_gpu": err}
     print(json.dumps(line), flush=True)
+
+
+def copy_ms(nbytes, reps, dev):
+    """Average ms of a device-to-device copy of `nbytes` (torch's copy kernel; bytes read + written = 2 * nbytes)."""
+    import torch
+
+    src = torch.empty(nbytes, dtype=torch.uint8, device=dev).fill_(1)
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(reps):
+        dst.copy_(src)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / reps
+    del src, dst
+    return ms
+
+
+def read_probe(nbytes, reps, dev):
+    """Best streaming-read rate of the probes in locals_amd/libread_probe.so over `nbytes` (GB/s), and the setting
+    that gave it.  Tried: direct buffer->LDS loads (the decode kernels' method) by 2048 / 4096 single-wave
+    workgroups with rings of 2, 3 and 4 16-KiB tiles, and plain 16-byte vector loads by 4096 workgroups of 256."""
+    import torch
+
+    from locals_amd import _lib
+
+    path = os.path.join(ROOT, "locals_amd", "libread_probe.so")
+    if not os.path.exists(path):
+        raise RuntimeError(f"{path} is missing: run python -m locals_amd.build")
+    lib = ctypes.CDLL(path)
+    V = ctypes.c_void_p
+    lib.lcl_probe_read_lds.argtypes = [V, ctypes.c_size_t, V, ctypes.c_int, ctypes.c_int, V]
+    lib.lcl_probe_read_vec.argtypes = [V, ctypes.c_size_t, V, ctypes.c_int, V]
+    lib.lcl_probe_out_words.restype = ctypes.c_size_t
+    lib.lcl_probe_out_words.argtypes = [ctypes.c_int]
+    src = torch.empty(nbytes, dtype=torch.uint8, device=dev).fill_(1)
+    out = torch.empty(int(lib.lcl_probe_out_words(4096)), dtype=torch.int32, device=dev)
+    stream = _lib.stream_of(dev)
+    settings = [("lds", w, d) for w in (2048, 4096) for d in (2, 3, 4)] + [("vec", 4096, 0)]
+    best = (0.0, None)
+    for kind, w, d in settings:
+        def launch():
+            if kind == "lds":
+                rc = lib.lcl_probe_read_lds(src.data_ptr(), nbytes, out.data_ptr(), w, d, stream)
+            else:
+                rc = lib.lcl_probe_read_vec(src.data_ptr(), nbytes, out.data_ptr(), w, stream)
+            if rc:
+                raise RuntimeError(f"read probe {kind} returned {rc}")
+
+        launch()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(reps):
+            launch()
+        e1.record()
+        torch.cuda.synchronize()
+        gbs = nbytes / (e0.elapsed_time(e1) / reps) / 1e6
+        print(f"read probe {kind} {w} {d}: {gbs:.1f} GB/s", file=sys.stderr, flush=True)
+        if gbs > best[0]:
+            what = f"{w} waves, LDS ring of {d} tiles" if kind == "lds" else f"{w} x 256 threads, vector loads"
+            best = (gbs, what)
+    del src, out
+    return best
 
 
 def _traffic(name, kernel):

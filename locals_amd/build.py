@@ -1,4 +1,5 @@
-"""Build recipe of liblocals_amd.so: every HIP source under csrc/ compiled for gfx950 into one shared library.
+"""Build recipe of liblocals_amd.so: every HIP source under csrc/ compiled for gfx950 into one shared library
+(plus libread_probe.so, the bench's streaming-read probe, from probe/read_probe.hip).
 
 Run ``python -m locals_amd.build`` (``__graft_entry__.build()`` calls ``build()``).  The library links the HIP
 runtime that torch ships (``torch/lib/libamdhip64.so``), so a process that already imported torch keeps a single
@@ -17,6 +18,9 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 OUT = os.path.join(HERE, "liblocals_amd.so")
+# the bench's streaming-read probe: a library of its own, outside the attention ABI
+PROBE_SRC = os.path.join(HERE, "probe", "read_probe.hip")
+PROBE_OUT = os.path.join(HERE, "libread_probe.so")
 BUILD = os.path.join(ROOT, "_build")
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
@@ -66,8 +70,13 @@ def build(verbose: bool = False) -> str:
         link[1:1] = [f"-L{tl}", f"-Wl,-rpath,{tl}"]
     _run(link)
     os.replace(OUT + ".tmp", OUT)
+    probe = [HIPCC, *FLAGS, "-shared", PROBE_SRC, "-o", PROBE_OUT + ".tmp"]
+    if tl:
+        probe[1:1] = [f"-L{tl}", f"-Wl,-rpath,{tl}"]
+    _run(probe)
+    os.replace(PROBE_OUT + ".tmp", PROBE_OUT)
     if verbose:
-        print("built", OUT)
+        print("built", OUT, "and", PROBE_OUT)
     return OUT
 
 

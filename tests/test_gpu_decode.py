@@ -178,26 +178,28 @@ def test_ragged_matches_oracle(dev, H, Hkv, kvdt):
     assert (_out(got)[2] == 0).all()
 
 
-@pytest.mark.parametrize("H,KVH", [(8, 2), (24, 4)])
-def test_attend_many_rows(dev, H, KVH):
-    """More than 64 rows (the quad pass 1 then scans the rows 64 at a time to split its work) with ragged left
-    padding, empty rows and a row whose keys start mid-tile."""
+@pytest.mark.parametrize("H,KVH,B", [(8, 2, 100), (24, 4, 100), (32, 8, 37), (32, 4, 64)])
+def test_attend_many_rows(dev, H, KVH, B):
+    """Many rows with ragged left padding, empty rows and a row whose keys start mid-tile.  Past 64 rows the quad
+    pass 1 scans the rows 64 at a time; up to 64 it holds one a lane, read 16 at a time by scalar loads (37 ends
+    inside a group of 16, 64 fills four)."""
     from locals_amd import qkv
 
-    g = rng(14 + H)
-    B, cap, n = 100, 640, 600
+    g = rng(14 + H + B)
+    cap, n = 640, 600
     q = normal16(g, (B, H, 1, 128))
     K, V = q8_cache(g, B, KVH, cap, kscale=2.0)
     sinks = normal16(g, (H,), 2.0)
     start = g.integers(0, n + 1, size=B).astype(np.int32)
-    start[[3, 40, 77]] = n  # empty rows
-    start[[5, 90]] = 0
+    empty = [3, B * 2 // 5, B * 3 // 4]
+    start[empty] = n  # empty rows
+    start[[5, B - 2]] = 0
     got = qkv.attend(to_torch(q, dev), triple_to_torch(K, dev), triple_to_torch(V, dev), n, to_torch(sinks, dev),
                      0.0884, to_torch(start, dev))
     torch.cuda.synchronize()
     ref = oattn.attend(q, K, V, n, sinks, 0.0884, start)
     assert np.abs(_out(got) - ref).max() <= 2e-3
-    assert not _out(got)[[3, 40, 77]].any()
+    assert not _out(got)[empty].any()
 
 
 def test_attend_c2_full_size_vs_c_restatement(dev):
