@@ -103,6 +103,40 @@ def test_dequantize(dev, odt):
     assert (err <= ulp).all()
 
 
+@pytest.mark.parametrize("D,sdt,odt", [(64, "float16", torch.float16), (128, "bfloat16", torch.float32),
+                                        (192, "float16", torch.float32), (256, "bfloat16", torch.bfloat16),
+                                        (512, "float16", torch.float16), (192, "bfloat16", torch.bfloat16)])
+def test_dequantize_is_one_fused_multiply_add(dev, D, sdt, odt):
+    """lcl_dequantize computes each value as one fp32 fused multiply-add scale * code + bias, then rounds it to the
+    output dtype.  That is pinned bit for bit for the kernel of D = 64 / 128 / 256 / 512 (row and group by shifts)
+    and the general one (D = 192).  The exact value is formed in float64 (scale * code has at most 19 significant
+    bits, so for these groups the sum is exact) and rounded once to fp32, as the fused operation does."""
+    from locals_amd import _lib
+
+    g = rng(6 + D)
+    rows = 333
+    x = normal16(g, (rows, D), 3.0, dtype=sdt)
+    w, sc, bi = oq.quantize(x, dtype=sdt)
+    s_t, b_t, w_t = to_torch(sc, dev, sdt), to_torch(bi, dev, sdt), to_torch(w, dev)
+    out = torch.empty((rows, D), dtype=odt, device=dev)
+    lib = _lib.load()
+    rc = lib.lcl_dequantize(_lib.ptr(w_t), _lib.ptr(s_t), _lib.ptr(b_t), _lib.dtype_code(s_t.dtype), rows, D,
+                            _lib.ptr(out), _lib.dtype_code(odt), _lib.stream_of(dev))
+    _lib.check(rc, "lcl_dequantize")
+    torch.cuda.synchronize()
+    codes = w.view(np.uint8).reshape(rows, D).astype(np.float64)
+    s64 = np.repeat(oq.to_f32(sc, sdt).astype(np.float64), 64, axis=1)
+    b64 = np.repeat(oq.to_f32(bi, sdt).astype(np.float64), 64, axis=1)
+    v32 = (s64 * codes + b64).astype(np.float32)
+    if odt == torch.float32:
+        want = torch.from_numpy(v32)
+    elif odt == torch.float16:
+        want = torch.from_numpy(v32.astype(np.float16))
+    else:
+        want = torch.from_numpy(oq.from_f32(v32, "bfloat16").view(np.int16)).view(torch.bfloat16)
+    assert torch.equal(out.cpu(), want)
+
+
 def test_batch_cache_decode_step_equals_oracle(dev):
     """A BatchQuantizedKVCache built by update_and_fetch then attended (qkv.attention, one query a row) equals the
     oracle over the oracle-quantized keys: the cache's codes are bit-exact and the attention within 2e-3."""
