@@ -191,7 +191,12 @@ def bench_multi(cfg, args, dev):
         pairs = sum(P + i + 1 for i in range(L))
     flops = pairs * H * 4 * 128
     kv_bytes = Bp * KVH * N * (512 if W else 272)
-    nbytes = int(lib.lcl_sdpa_workspace_bytes(Bp, H, L, N, sdpa.BLOCK))
+    split = int(lib.lcl_sdpa_workspace_bytes(Bp, H, L, N, sdpa.BLOCK))
+    nbytes = int(lib.lcl_sdpa_workspace_bytes_kv(Bp, H, KVH, L, N, cap, sdpa.BLOCK, 1 if W else 0, mk))
+    if not sdpa.DEQUANTIZE_FIRST:
+        nbytes = split
+    # with room for it the library dequantizes K/V once and runs the 16-bit kernel; its events then span both
+    route = "dequantize K/V, 16-bit pass 1" if nbytes > split else ("16-bit pass 1" if W else "fused 8-bit pass 1")
     ws = torch.empty(nbytes // 4 + 1, dtype=torch.float32, device=dev)
     out = torch.empty((Bp, H, L, 128), dtype=torch.bfloat16 if W else torch.float16, device=dev)
     ev = Events(2 * args.steps + 2)
@@ -218,7 +223,7 @@ def bench_multi(cfg, args, dev):
     t = np.array([ev.ms(2 * i, 2 * i + 1) for i in range(args.steps)])
     ev.close()
     us = float(t.mean() * 1e3)
-    res = {"kernel": "sdpa_pass1", "L": L, "N": N, "rows": Bp, "avg_us": round(us, 2),
+    res = {"kernel": "sdpa_pass1", "route": route, "L": L, "N": N, "rows": Bp, "avg_us": round(us, 2),
            "tflops": round(flops / (us * 1e-6) / 1e12, 1), "mfma_frac_of_2.5PF": round(flops / (us * 1e-6) / 2.5e15, 4),
            "kv_GBs": round(kv_bytes / (us * 1e-6) / 1e9, 1), "flops": flops, "kv_bytes": kv_bytes}
     if cfg["name"] == "c5":

@@ -98,6 +98,17 @@ int lcl_dequantize(const uint32_t* words, const void* scales, const void* biases
  * pass 1 writes the output itself and the workspace pointer may be NULL. */
 size_t lcl_sdpa_workspace_bytes(int B, int H, int L, int N, int block);
 
+/* Bytes of workspace for lcl_sdpa given the K/V format and mask as well: the split-K
+ * bytes above, plus -- when the library takes its dequantize-first route for this call --
+ * room for K and V dequantized to 16 bits, 2 * B * KVH * cap * 128 * 2 bytes after the
+ * split-K part (rounded up to 256).  That route is taken for 8-bit K/V, any mask but the
+ * sliding window, at least 16 row blocks per (row, KV head) and cap - N <= 512: the reference's
+ * own prompt path dequantizes the whole prefix first too (locals/qkv.py:270-272).  A smaller
+ * workspace (lcl_sdpa_workspace_bytes) keeps the fused 8-bit kernel; both give the same
+ * values.  No counterpart in the reference. */
+size_t lcl_sdpa_workspace_bytes_kv(int B, int H, int KVH, int L, int N, int cap, int block, int kvfmt,
+                                   int mask_kind);
+
 /* MLX scaled_dot_product_attention(q, k, v, scale, mask, sinks) as the reference
  * routes its multi-query variants through it: the 8-bit prefill/span branch of
  * qkv.attention -> fuse.attend_few over dequantized K/V (locals/qkv.py:270-272,

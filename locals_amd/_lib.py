@@ -35,6 +35,7 @@ SIGNATURES = {
     "lcl_quantize_append": (I, [P, P, I, P, P, P, P, P, P, I, I, I, I, I, I, I, P]),
     "lcl_dequantize": (I, [P, P, P, I, ctypes.c_longlong, I, P, I, P]),
     "lcl_sdpa_workspace_bytes": (Z, [I, I, I, I, I]),
+    "lcl_sdpa_workspace_bytes_kv": (Z, [I, I, I, I, I, I, I, I, I]),
     "lcl_sdpa": (I, [P, I, I, P, P, P, P, P, P, P, P, I, P, I, I, P, LL, P, LL, LL, LL, LL, P, F, I, I, I, I, I, I, I, I,
                      P, P, Z, P]),
     "lcl_sdpa_ex": (I, [P, I, I, P, P, P, P, P, P, P, P, I, P, I, I, P, LL, P, LL, LL, LL, LL, P, F, I, I, I, I, I, I, I,

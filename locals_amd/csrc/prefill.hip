@@ -715,12 +715,43 @@ static int sdpa_chunk(int block, int B, int H, int L, int N, int wg_rows) {
   return ((tiles + want - 1) / want) * kKT;
 }
 
+// Row tiles a wave: two (128 rows a workgroup) when there are more than 64 rows, halving the operand reads (and,
+// 8-bit, the dequantization) per row; one under a dense mask, and for 8-bit under a window (their per-key tests
+// would not fit beside two tiles' registers).
+static int sdpa_row_tiles(int rows, int mask_kind, int kvfmt) {
+  return (rows > 64 && mask_kind != MK_DENSE && (kvfmt == KV_16 || mask_kind != MK_WINDOW)) ? 2 : 1;
+}
+
+// Whether an 8-bit call dequantizes K and V once into the workspace and runs the 16-bit kernel over them.  The
+// fused kernel dequantizes every tile in each workgroup that reads it, i.e. once per row block of a (row, KV head);
+// from 16 row blocks one pass over the cache costs less (C4's 512-query causal chunk over 16k keys: 199 us fused
+// against 26.5 + 161 us).  Not under a window (a workgroup reads only its band of keys), nor when the buffers hold
+// many positions past N (the pass covers every position up to cap).
+static bool sdpa_dequantize_first(int kvfmt, int mask_kind, int H, int KVH, int L, int N, int cap) {
+  if (kvfmt != KV_Q8 || mask_kind == MK_WINDOW || N <= 0 || cap - N > 512) return false;
+  const int rows = L * (H / KVH);
+  const int rt = sdpa_row_tiles(rows, mask_kind, KV_16);
+  return (rows + 64 * rt - 1) / (64 * rt) >= 16;
+}
+
+// the dequantized K and V of that route: two (B, KVH, cap, 128) buffers of 16-bit values
+static size_t sdpa_dq_bytes(int B, int KVH, int cap) { return 2 * size_t(B) * KVH * cap * kD * 2; }
+static size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+
 extern "C" {
 
 size_t lcl_sdpa_workspace_bytes(int B, int H, int L, int N, int block) {
   const int chunk = sdpa_chunk(block, B, H, L, N, 128);  // 128-row workgroups take the most chunks
   const int nchunks = N > 0 ? (N + chunk - 1) / chunk : 1;
   return nchunks > 1 ? size_t(B) * H * L * nchunks * (2 + kD) * sizeof(float) : 0;
+}
+
+size_t lcl_sdpa_workspace_bytes_kv(int B, int H, int KVH, int L, int N, int cap, int block, int kvfmt,
+                                   int mask_kind) {
+  const size_t split = lcl_sdpa_workspace_bytes(B, H, L, N, block);
+  if (B <= 0 || KVH <= 0 || H % KVH || cap <= 0 || !sdpa_dequantize_first(kvfmt, mask_kind, H, KVH, L, N, cap))
+    return split;
+  return align256(split) + sdpa_dq_bytes(B, KVH, cap);
 }
 
 int lcl_sdpa_ex(const void* q, int qdt, int kvfmt, const uint32_t* kw, const void* ks, const void* kb,
@@ -748,11 +779,8 @@ int lcl_sdpa_ex(const void* q, int qdt, int kvfmt, const uint32_t* kw, const voi
   if (mask_kind == MK_WINDOW && window <= 0) return -1;
   if (mask_kind == MK_TREE && (!tree || L > 64 || L > N)) return -2;
   if (mask_kind == MK_DENSE && !dense) return -1;
-  // row tiles a wave: two (128 rows a workgroup) when there are more than 64 rows, halving the operand reads (and,
-  // 8-bit, the dequantization) per row; one under a dense mask, and for 8-bit under a window (their per-key
-  // tests would not fit beside two tiles' registers)
   const int rows = L * (H / KVH);
-  const int rt = (rows > 64 && mask_kind != MK_DENSE && (kvfmt == KV_16 || mask_kind != MK_WINDOW)) ? 2 : 1;
+  const int rt = sdpa_row_tiles(rows, mask_kind, kvfmt);
   int chunk = sdpa_chunk(block, B, H, L, N, 64 * rt);
   int nchunks = N > 0 ? (N + chunk - 1) / chunk : 1;
   if (mask_kind == MK_WINDOW && N > 0) {
@@ -764,6 +792,23 @@ int lcl_sdpa_ex(const void* q, int qdt, int kvfmt, const uint32_t* kw, const voi
   }
   const size_t need = nchunks > 1 ? size_t(B) * H * L * nchunks * (2 + kD) * sizeof(float) : 0;
   if (need && (!workspace || workspace_bytes < need)) return -3;
+  hipEvent_t e0 = static_cast<hipEvent_t>(ev_start), e1 = static_cast<hipEvent_t>(ev_stop);
+  // the dequantize-first route, when the caller's workspace has room for it (lcl_sdpa_workspace_bytes_kv); the
+  // 16-bit kernel takes the same row tiles and chunks, so the split-K part of the workspace is unchanged
+  const bool dq = sdpa_dequantize_first(kvfmt, mask_kind, H, KVH, L, N, cap) && workspace &&
+                  workspace_bytes >= align256(need) + sdpa_dq_bytes(B, KVH, cap);
+  if (dq) {
+    _Float16* kd = reinterpret_cast<_Float16*>(static_cast<uint8_t*>(workspace) + align256(need));
+    _Float16* vd = kd + size_t(B) * KVH * cap * kD;
+    if (e0) hipEventRecord(e0, stream);
+    const long long kvrows = (long long)B * KVH * cap;
+    int rc = lcl_dequantize(kw, ks, kb, kvdt, kvrows, kD, kd, kvdt, stream);
+    if (rc == 0) rc = lcl_dequantize(vw, vs, vb, kvdt, kvrows, kD, vd, kvdt, stream);
+    if (rc) return rc;
+    kvfmt = KV_16;
+    kf = kd;
+    vf = vd;
+  }
   SdpaParams p{};
   p.q = q;
   p.kw = kw; p.ks = ks; p.kb = kb; p.vw = vw; p.vs = vs; p.vb = vb; p.kf = kf; p.vf = vf;
@@ -779,13 +824,18 @@ int lcl_sdpa_ex(const void* q, int qdt, int kvfmt, const uint32_t* kw, const voi
   p.nchunks = nchunks; p.chunk = chunk; p.mask = mask_kind; p.window = window;
   p.direct = nchunks == 1; p.out = out; p.odt = qdt;
   p.nrowblocks = (rows + 64 * rt - 1) / (64 * rt);
-  hipEvent_t e0 = static_cast<hipEvent_t>(ev_start), e1 = static_cast<hipEvent_t>(ev_stop);
+  hipEvent_t dq_stop = nullptr;
+  if (dq) {  // the events span the dequantization and pass 1: the start went in before the dequantization
+    dq_stop = e1;
+    e0 = e1 = nullptr;
+  }
   {  // with no key in reach every workgroup records empty parts, so the combine needs no cleared workspace
     const long long total = (long long)nchunks * p.nrowblocks * B * KVH;  // one-dimensional, mapped per XCD
     if (total > (1LL << 30)) return -2;
     const dim3 grid(unsigned((total + 7) / 8 * 8));
     if (kvfmt == KV_Q8) launch_fmt<KV_Q8>(qdt, kvdt, rt, grid, stream, e0, e1, p);
     else launch_fmt<KV_16>(qdt, kvdt, rt, grid, stream, e0, e1, p);
+    if (dq_stop) hipEventRecord(dq_stop, stream);
   }
   if (!p.direct) {
     SdpaCombineParams c{p.pm, p.pl, p.po, sinks, out, B * H * L, H, L, nchunks, qdt};

@@ -24,6 +24,9 @@ from . import _lib
 from .qkv import _words_ok
 
 BLOCK = 0  # keys a pass-1 workgroup reads (a multiple of 64); 0: the library's choice
+# 8-bit K/V with many row blocks per (row, KV head): give the library room to dequantize K and V once and run the
+# 16-bit kernel (the reference's own prompt path dequantizes first too); False keeps the fused 8-bit kernel
+DEQUANTIZE_FIRST = True
 
 MASK_NONE, MASK_CAUSAL, MASK_TREE, MASK_DENSE, MASK_WINDOW = 0, 1, 2, 3, 4
 
@@ -187,7 +190,10 @@ def scaled_dot_product_attention(q: torch.Tensor, k, v, *, scale: float, mask=No
     st = None if start is None else start.to(device=dev, dtype=torch.int32).contiguous()
     lib = _lib.load()
     blk = int(BLOCK)
-    nbytes = int(lib.lcl_sdpa_workspace_bytes(B, H, L, N, blk))
+    if DEQUANTIZE_FIRST:
+        nbytes = int(lib.lcl_sdpa_workspace_bytes_kv(B, H, KVH, L, N, cap, blk, fmt, mk))
+    else:
+        nbytes = int(lib.lcl_sdpa_workspace_bytes(B, H, L, N, blk))
     ws = torch.empty(nbytes // 4 + 1, dtype=torch.float32, device=dev)
     out = torch.empty((B, H, L, D), dtype=q.dtype, device=dev)
     P = _lib.ptr

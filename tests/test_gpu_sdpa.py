@@ -107,6 +107,55 @@ def test_sdpa_16bit(dev, kvdt, masked):
     assert np.abs(_np(got) - ref).max() <= _tol(ref, kvdt)
 
 
+@pytest.mark.parametrize("case", ["causal-float16", "dense-bfloat16"])
+def test_dequantize_first_route(dev, sdpa_block, case):
+    """8-bit K/V with 16 or more row blocks per (row, KV head): given the room (lcl_sdpa_workspace_bytes_kv) the
+    library dequantizes K and V once and runs the 16-bit kernel.  Its output equals the fused 8-bit kernel's bit for
+    bit -- the same 16-bit operand values through the same products -- and the oracle within the bar, here with left
+    padding and sinks."""
+    from locals_amd import _lib, sdpa
+
+    masked, dtype = case.split("-")
+    g = rng(31 if masked == "causal" else 32)
+    if masked == "causal":  # 512 queries x 4 heads = 16 blocks of 128 rows
+        B, H, KVH, L, N = 1, 32, 8, 512, 700
+    else:  # dense masks take 64-row blocks: 256 queries x 4 heads = 16
+        B, H, KVH, L, N = 2, 16, 4, 256, 400
+    cap = (N + 255) // 256 * 256
+    print(f"dequantize-first {case} B={B} H={H} KVH={KVH} L={L} N={N} block={sdpa_block}", flush=True)
+    lib = _lib.load()
+    mk = sdpa.MASK_CAUSAL if masked == "causal" else sdpa.MASK_DENSE
+    assert lib.lcl_sdpa_workspace_bytes_kv(B, H, KVH, L, N, cap, sdpa_block, 0, mk) > \
+        lib.lcl_sdpa_workspace_bytes(B, H, L, N, sdpa_block)
+    q = normal16(g, (B, H, L, 128), dtype=dtype)
+    K, V = q8_cache(g, B, KVH, cap, kscale=2.0, dtype=dtype)
+    sinks = normal16(g, (H,), 2.0, dtype=dtype)
+    start = np.array([37, 0][:B], np.int32)
+    if masked == "causal":
+        mask = "causal"
+        vis = oa.causal_mask(L, N)[None, None]
+    else:
+        vis = g.random((B, 1, L, N)) < 0.6
+        vis[..., N - 1] = True
+        mask = torch.from_numpy(vis).to(dev)
+    vis = vis & (np.arange(N)[None, None, None, :] >= start[:, None, None, None])
+    Kt, Vt = triple_to_torch(K, dev, dtype), triple_to_torch(V, dev, dtype)
+    args = (to_torch(q, dev, dtype), tuple(a[:, :, :N] for a in Kt), tuple(a[:, :, :N] for a in Vt))
+    kw = dict(scale=0.0884, mask=mask, sinks=to_torch(sinks, dev, dtype), start=to_torch(start, dev))
+    got = sdpa.scaled_dot_product_attention(*args, **kw)
+    old = sdpa.DEQUANTIZE_FIRST
+    sdpa.DEQUANTIZE_FIRST = False
+    try:
+        fused = sdpa.scaled_dot_product_attention(*args, **kw)
+    finally:
+        sdpa.DEQUANTIZE_FIRST = old
+    torch.cuda.synchronize()
+    assert torch.equal(got, fused)
+    if sdpa_block == 0:  # the oracle once per case (the chunkings are tied to it by the other tests)
+        ref = oa.sdpa_q8(q, K, V, 0.0884, vis, sinks, n=N, dtype=dtype)
+        assert np.abs(_np(got) - ref).max() <= _tol(ref, dtype)
+
+
 def test_left_padding_start(dev):
     """start[b] masks the keys before it, like the batch cache's left padding."""
     from locals_amd.sdpa import scaled_dot_product_attention
