@@ -191,4 +191,8 @@ __device__ __forceinline__ void lds_load4(BufRsrc r, void* lds, uint32_t voff) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)(lds), 4, voff, 0, 0, AUX);
 }
 
+// quant.hip: K and V (rows of 128 values) of an 8-bit cache dequantized to the scales' 16-bit dtype in one launch
+int dequantize_kv128(const uint32_t* kw, const void* ks, const void* kb, const uint32_t* vw, const void* vs,
+                     const void* vb, int sdt, long long rows, void* kout, void* vout, hipStream_t stream);
+
 }  // namespace lcl

@@ -801,9 +801,7 @@ int lcl_sdpa_ex(const void* q, int qdt, int kvfmt, const uint32_t* kw, const voi
     _Float16* kd = reinterpret_cast<_Float16*>(static_cast<uint8_t*>(workspace) + align256(need));
     _Float16* vd = kd + size_t(B) * KVH * cap * kD;
     if (e0) hipEventRecord(e0, stream);
-    const long long kvrows = (long long)B * KVH * cap;
-    int rc = lcl_dequantize(kw, ks, kb, kvdt, kvrows, kD, kd, kvdt, stream);
-    if (rc == 0) rc = lcl_dequantize(vw, vs, vb, kvdt, kvrows, kD, vd, kvdt, stream);
+    const int rc = dequantize_kv128(kw, ks, kb, vw, vs, vb, kvdt, (long long)B * KVH * cap, kd, vd, stream);
     if (rc) return rc;
     kvfmt = KV_16;
     kf = kd;

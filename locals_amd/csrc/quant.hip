@@ -114,7 +114,7 @@ __global__ __launch_bounds__(256) void dequantize_rows(DequantParams p) {
 // wave is contiguous; a block covers 1024 consecutive words.  Rows of D = 4 << WSH values, so the row and group of a
 // word come from shifts.  The same arithmetic as dequantize_rows.
 template <int WSH>
-__global__ __launch_bounds__(256) void dequantize_rows_p2(DequantParams p) {
+__device__ __forceinline__ void dequantize_p2_block(const DequantParams& p) {
   const long long nw = p.rows << WSH;
   const long long w0 = static_cast<long long>(blockIdx.x) * 1024 + threadIdx.x;
 #pragma unroll
@@ -128,6 +128,29 @@ __global__ __launch_bounds__(256) void dequantize_rows_p2(DequantParams p) {
     store4_from_f32(p.out, wid * 4, s * float(x & 0xffu) + b, s * float((x >> 8) & 0xffu) + b,
                     s * float((x >> 16) & 0xffu) + b, s * float(x >> 24) + b, p.odt);
   }
+}
+template <int WSH>
+__global__ __launch_bounds__(256) void dequantize_rows_p2(DequantParams p) {
+  dequantize_p2_block<WSH>(p);
+}
+// K and V of a cache in one launch: blockIdx.y picks the buffer
+struct DequantPair {
+  DequantParams d[2];
+};
+template <int WSH>
+__global__ __launch_bounds__(256) void dequantize_pair_p2(DequantPair pp) {
+  dequantize_p2_block<WSH>(blockIdx.y ? pp.d[1] : pp.d[0]);
+}
+
+// K and V (rows of 128 values each) of an 8-bit cache dequantized to 16 bits in one launch.  Declared in
+// lcl_common.h for the masked-attention entry point; 0 or a hipError_t.
+int dequantize_kv128(const uint32_t* kw, const void* ks, const void* kb, const uint32_t* vw, const void* vs,
+                     const void* vb, int sdt, long long rows, void* kout, void* vout, hipStream_t stream) {
+  DequantPair pp{{{kw, ks, kb, kout, rows, 128, sdt, sdt}, {vw, vs, vb, vout, rows, 128, sdt, sdt}}};
+  const long long blocks = (rows * 32 + 1023) / 1024;
+  if (blocks > 0x7fffffffLL) return int(hipErrorInvalidValue);
+  hipLaunchKernelGGL(dequantize_pair_p2<5>, dim3(static_cast<unsigned>(blocks), 2), dim3(256), 0, stream, pp);
+  return int(hipGetLastError());
 }
 
 }  // namespace lcl
