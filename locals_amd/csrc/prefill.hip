@@ -381,6 +381,21 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 
   // Each K / V^T operand fragment is read from LDS once and applied to every row tile of the wave, so a
   // fragment is live for RT MFMAs only (the row tiles' scores, P and O are what stays in registers).
+  // whether row tile r's row (this lane's) sees key j
+  auto key_visible = [&](int r, int j) __attribute__((always_inline)) -> bool {
+    bool ok = real[r] & (j >= klo) & (j < khi);
+    if constexpr (MASK == MK_CAUSAL) ok = ok & (j <= p.N - p.L + qi[r]);
+    if constexpr (MASK == MK_WINDOW) {
+      const int pos = p.N - p.L + qi[r];
+      ok = ok & (j <= pos) & (j > pos - p.window);
+    }
+    if constexpr (MASK == MK_TREE) {
+      const int d = j - (p.N - p.L);
+      ok = ok & ((d < 0) | (((tbits[r] >> (d & 63)) & 1ull) != 0ull));
+    }
+    if constexpr (MASK == MK_DENSE) ok = ok & (drow[r][min(max(j, 0), p.N - 1) * p.msk] != 0);
+    return ok;
+  };
   auto compute = [&](int t0, const uint8_t* S) __attribute__((always_inline)) {
     // S^T = K Q^T: st[r][t][i] = S[row][t0 + 16 t + 4 q4 + i].  Where registers allow (causal mask, one row
     // tile), the 32-dim step kk is the outer loop, so the 4 RT accumulators are independent chains and a step's
@@ -391,10 +406,41 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     for (int t = 0; t < 4; t++)
 #pragma unroll
       for (int r = 0; r < RT; r++) st[r][t] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+    // a tile every key of which every row of the wave sees needs no mask (for causal prefill, all but the
+    // diagonal tiles); rows past the row count are not written, so they need none either
+    bool full = t0 >= klo && t0 + kKT <= khi;
+    if constexpr (MASK == MK_CAUSAL) full = full && t0 + kKT - 1 <= p.N - p.L + wave_q0;
+    if constexpr (MASK == MK_TREE) full = full && t0 + kKT <= p.N - p.L;
+    if constexpr (MASK == MK_WINDOW)  // causal for the wave's first query, in the window of its last
+      full = full && t0 + kKT - 1 <= p.N - p.L + wave_q0 &&
+             t0 > p.N - p.L + (row0 + 64 * (RT - 1) + 16 * wave + 15) / p.G - p.window;
+    if constexpr (MASK == MK_DENSE) full = false;
     if constexpr (kStepOuter) {
+      // The mask enters as the accumulators' initial value (0 or -inf), so the scores need no pass after the
+      // products and a full tile's first step takes the constant 0.  Every key row of the tile is finite: rows
+      // outside [klo, khi) were cleared in the slot (16-bit) or dequantized as 0 (8-bit).
+      uint4 kf[4];
 #pragma unroll
-      for (int kk = 0; kk < 4; kk++) {
-        uint4 kf[4];
+      for (int t = 0; t < 4; t++) kf[t] = kfrag(S, t, 0);
+      if (full) {
+#pragma unroll
+        for (int t = 0; t < 4; t++)
+#pragma unroll
+          for (int r = 0; r < RT; r++) st[r][t] = mma32<MT>(kf[t], qb[r][0], st[r][t]);
+      } else {
+#pragma unroll
+        for (int r = 0; r < RT; r++)
+#pragma unroll
+          for (int t = 0; t < 4; t++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) st[r][t][i] = key_visible(r, t0 + 16 * t + 4 * q4 + i) ? 0.0f : -INFINITY;
+#pragma unroll
+        for (int t = 0; t < 4; t++)
+#pragma unroll
+          for (int r = 0; r < RT; r++) st[r][t] = mma32<MT>(kf[t], qb[r][0], st[r][t]);
+      }
+#pragma unroll
+      for (int kk = 1; kk < 4; kk++) {
 #pragma unroll
         for (int t = 0; t < 4; t++) kf[t] = kfrag(S, t, kk);
 #pragma unroll
@@ -412,20 +458,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
           for (int r = 0; r < RT; r++) st[r][t] = mma32<MT>(kf, qb[r][kk], st[r][t]);
         }
     }
-    // a tile every key of which every row of the wave sees needs no mask (for causal prefill, all but the
-    // diagonal tiles); rows past the row count are not written, so they need none either
-    bool full = t0 >= klo && t0 + kKT <= khi;
-    if constexpr (MASK == MK_CAUSAL) full = full && t0 + kKT - 1 <= p.N - p.L + wave_q0;
-    if constexpr (MASK == MK_TREE) full = full && t0 + kKT <= p.N - p.L;
-    if constexpr (MASK == MK_WINDOW)  // causal for the wave's first query, in the window of its last
-      full = full && t0 + kKT - 1 <= p.N - p.L + wave_q0 &&
-             t0 > p.N - p.L + (row0 + 64 * (RT - 1) + 16 * wave + 15) / p.G - p.window;
-    if constexpr (MASK == MK_DENSE) full = false;
     uint4 pb[RT][2];  // P^T as B operands: k index 8 q4 + j <-> key 32 u + (j < 4 ? 4 q4 + j : 16 + 4 q4 + j - 4)
 #pragma unroll
     for (int r = 0; r < RT; r++) {
       float tmax = -INFINITY;
-      if (full) {
+      if (kStepOuter || full) {
 #pragma unroll
         for (int t = 0; t < 4; t++)
           tmax = fmaxf(tmax, fmaxf(fmaxf(st[r][t][0], st[r][t][1]), fmaxf(st[r][t][2], st[r][t][3])));
@@ -434,19 +471,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         for (int t = 0; t < 4; t++) {
 #pragma unroll
           for (int i = 0; i < 4; i++) {
-            const int j = t0 + 16 * t + 4 * q4 + i;
-            bool ok = real[r] & (j >= klo) & (j < khi);
-            if constexpr (MASK == MK_CAUSAL) ok = ok & (j <= p.N - p.L + qi[r]);
-            if constexpr (MASK == MK_WINDOW) {
-              const int pos = p.N - p.L + qi[r];
-              ok = ok & (j <= pos) & (j > pos - p.window);
-            }
-            if constexpr (MASK == MK_TREE) {
-              const int d = j - (p.N - p.L);
-              ok = ok & ((d < 0) | (((tbits[r] >> (d & 63)) & 1ull) != 0ull));
-            }
-            if constexpr (MASK == MK_DENSE) ok = ok & (drow[r][min(max(j, 0), p.N - 1) * p.msk] != 0);
-            const float sc = ok ? st[r][t][i] : -INFINITY;
+            const float sc = key_visible(r, t0 + 16 * t + 4 * q4 + i) ? st[r][t][i] : -INFINITY;
             st[r][t][i] = sc;
             tmax = fmaxf(tmax, sc);
           }
@@ -545,14 +570,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         dma16(dv16, ls + 16384u + 1024u * uint32_t(4 * wave + u), voff);
       }
     };
-    // a tile reaching past [klo, khi): the V rows of keys outside it are cleared (rows past n or before start
-    // may hold anything, and 0 * inf is not 0); their K rows only give scores that the mask discards
+    // a tile reaching past [klo, khi): the K and V rows of keys outside it are cleared (rows past n or before
+    // start may hold anything, 0 * inf is not 0, and a masked score starts at -inf, which a NaN product would undo)
     auto clear_v = [&](int t0, uint8_t* S) __attribute__((always_inline)) {
       const int key = tid >> 2, kg = t0 + key;
       if (kg < klo || kg >= khi) {
         uint4* row = reinterpret_cast<uint4*>(S + 16384 + key * 256 + 64 * (tid & 3));
+        uint4* krow = reinterpret_cast<uint4*>(S + key * 256 + 64 * (tid & 3));
 #pragma unroll
-        for (int i = 0; i < 4; i++) row[i] = make_uint4(0u, 0u, 0u, 0u);
+        for (int i = 0; i < 4; i++) row[i] = krow[i] = make_uint4(0u, 0u, 0u, 0u);
       }
     };
     auto step = [&](int t0, uint8_t* S) __attribute__((always_inline)) {
