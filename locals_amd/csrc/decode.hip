@@ -12,8 +12,7 @@
 //    over all (row, kv head, 64-key tile) work, one wave a workgroup, tiles by direct
 //    buffer->LDS loads, Q K^T on the 4x4x4 MFMA so no lane computes a padding head (one
 //    or two groups of 4 heads); described where it is defined.
-//  * qkv_pass1_q8 (8-bit, G > 8), below; qkv_pass1_q8_lds an LDS-staged form of it,
-//    kept for comparisons (LOCALS_AMD_DECODE=lds).
+//  * qkv_pass1_q8 (8-bit, G > 8), below.
 //  * ragged_pass1_16 (16-bit K/V, ragged rows).
 //
 // qkv_pass1_q8 (one workgroup = 4 waves = one (row, kv head, head slice, key
@@ -27,13 +26,18 @@
 //  * The score tile comes out of the MFMA as D[key][head]; that is exactly the A
 //    layout of the P V product (lane = head, 4 consecutive keys), so P never
 //    moves between lanes.  P V on MFMA: A = w = p * vscale (per key and group)
-//    split into fp16 hi + lo (relative error 2^-21, i.e. fp32-grade weights),
-//    B = V codes as 1024 + code, transposed from 4 keys' words by v_perm.  The
-//    bias and the 1024 offset go into one fp32 accumulator per (head, group):
+//    split into fp16 hi + lo, both rounded to nearest, B = V codes as 1024 + code,
+//    transposed from 4 keys' words by v_perm.  The bias and the 1024 offset go into
+//    one fp32 accumulator per (head, group):
 //        o_d = sum_t w_t (1024 + c_td) + sum_t (p_t b_t - 1024 w_t).
 //  * Online softmax in base 2, lazily rescaled: the running max only moves when
-//    a tile's max exceeds it by more than 2^6, so p <= 64 and w stays in fp16
-//    range; the rescale is a wave-uniform branch taken a handful of times.
+//    a tile's max exceeds it by more than 2^6, so p <= 64; the rescale is a
+//    wave-uniform branch taken a handful of times.  p is taken against the max
+//    minus a wave-uniform exponent E (lcl_common.h, "prescale"), chosen from the
+//    largest V scale seen so that w < 2^15: the weights that matter then have a
+//    normal fp16 hi and lo (relative error 2^-22), where at E = 0 small weights
+//    would lose their lo half to fp16 subnormals, a loss the (1024 + code) factor
+//    multiplies.  l, o and the side sums carry the same 2^E.
 //  * The 4 waves' partials are joined in LDS into one (m, l, o[128]) per (row,
 //    head, chunk); pass 2 joins the chunks with the sink.
 // Loads: per 16-key tile a lane issues 2 x 128-bit loads of K codes, 8 x 32-bit
@@ -244,7 +248,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
   const float C = p.scale_log2;
   const float zc0 = 1024.0f * qs0 * C, zc1 = 1024.0f * qs1 * C, qc0 = qs0 * C, qc1 = qs1 * C;
 
-  float m_run = -INFINITY, l_acc = 0.0f, wb0 = 0.0f, wb1 = 0.0f;
+  // lazy running max, the reference the weights are taken against (m_run - pE), sums; pE is the wave-uniform
+  // prescale exponent of the V weights (lcl_common.h) and pthr the least V-scale magnitude that needs it lowered
+  float m_run = -INFINITY, mref = -INFINITY, l_acc = 0.0f, wb0 = 0.0f, wb1 = 0.0f;
+  int pE = kPreInit, pthr = pre_thr<SDT>(kPreInit);
   f4 O[8];
 #pragma unroll
   for (int ii = 0; ii < 8; ii++) O[ii] = f4{0.0f, 0.0f, 0.0f, 0.0f};
@@ -303,9 +310,24 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
     tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
     tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
     const bool need = tmax > m_run + kRescaleThr;
-    if (__any(need)) {
-      const float corr = need ? (m_run == -INFINITY ? 0.0f : fast_exp2(m_run - tmax)) : 1.0f;
+    // largest |V scale| of this lane's valid keys (both groups): a scale at or above pthr needs pE lowered
+    uint32_t vmag = 0;
+#pragma unroll
+    for (int i = 0; i < 4; i++) vmag = mag_max2(vmag, valid[i] ? vsc[i] : 0u);
+    vmag = mag_fold(vmag);
+    const bool needE = int(vmag) >= pthr;
+    if (__any(need || needE)) {
+      if (__any(needE)) {  // the tile's largest scale (the lanes of a 16-lane row hold the same keys)
+        uint32_t x = vmag;
+        x = max(x, uint32_t(__shfl_xor(int(x), 16)));
+        x = max(x, uint32_t(__shfl_xor(int(x), 32)));
+        pE = min(pE, 9 - scale_exp<SDT>(uint32_t(__builtin_amdgcn_readfirstlane(int(x)))));
+        pthr = pre_thr<SDT>(pE);
+      }
       if (need) m_run = tmax;
+      const float nref = m_run - float(pE);
+      const float corr = mref == -INFINITY ? 0.0f : fast_exp2(mref - nref);
+      mref = nref;
       l_acc *= corr;
       wb0 *= corr;
       wb1 *= corr;
@@ -319,7 +341,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
     float w0[4], w1[4];
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-      float pr = fast_exp2(s[i] - m_run);
+      float pr = fast_exp2(s[i] - mref);
       float x0 = pr * hpart<SDT>(vsc[i], 0), x1 = pr * hpart<SDT>(vsc[i], 1);
       float y0 = pr * hpart<SDT>(vbi[i], 0), y1 = pr * hpart<SDT>(vbi[i], 1);
       if constexpr (MASKED) {  // garbage scales of masked keys must not reach the sums (0 * inf)
@@ -381,7 +403,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
   __shared__ float s_m[kWaves][16], s_l[kWaves][16];
   __shared__ float s_o[kWaves][16][kHD];
   if (q4 == 0) {
-    s_m[wave][c16] = m_run;
+    s_m[wave][c16] = mref;
     s_l[wave][c16] = l_acc;
   }
 #pragma unroll
@@ -389,269 +411,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
     const float b0 = __shfl(wb0, 4 * q4 + i), b1 = __shfl(wb1, 4 * q4 + i);
 #pragma unroll
     for (int ii = 0; ii < 8; ii++) s_o[wave][4 * q4 + i][64 * (ii >> 2) + 4 * c16 + (ii & 3)] = O[ii][i] + (ii < 4 ? b0 : b1);
-  }
-  __syncthreads();
-  join_waves(p, s_m, s_l, s_o, Gs, r, head0, c);
-}
-
-// ------------------------------------------------- 8-bit pass 1, LDS-staged
-// The workgroup streams its chunk in 64-key blocks through a 3-deep LDS ring filled by
-// direct buffer->LDS loads (whole 128-byte lines per instruction, non-temporal): a block is
-// K codes (8 KB, 16-byte chunks XOR-swizzled by key so operand reads spread over the banks),
-// V codes (8 KB, same swizzle) and the 64 keys' K/V scales and biases (4 x 256 B).  Each wave
-// issues 5 of a block's 20 load instructions; two blocks are in flight while one is computed.
-// Wave w computes the 16-key tile w of each block exactly as the register-fed kernel does,
-// reading its MFMA operands from LDS.  One barrier a block: each wave first waits for its own
-// loads of the block (vmcnt), the barrier then makes every wave's loads visible and frees the
-// slot the next load overwrites.
-constexpr int kBlk = 64;                        // keys a block
-constexpr int kBlkBytes = 8192 + 8192 + 4 * 256; // K codes, V codes, ks/kb/vs/vb
-constexpr int kRing = 3;  // blocks in the ring
-
-
-template <int QDT, int SDT>
-__global__ __launch_bounds__(256) void qkv_pass1_q8_lds(DecodeParams p) {
-  const int c = blockIdx.x;
-  const int kvh = blockIdx.y / p.nslices, sl = blockIdx.y % p.nslices;
-  const int r = blockIdx.z;
-  int lo, hi;
-  row_range(p.start, p.nkeys, p.n, p.cap, r, lo, hi);
-  const int c0 = c * p.chunk;
-  const int clo = max(lo, c0), chi = min(hi, c0 + p.chunk);
-  if (clo >= chi) return;  // uniform: no key of this row in this chunk
-
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
-  const int c16 = lane & 15, q4 = lane >> 4;
-  const int Gs = min(16, p.G - sl * 16);
-  const int head0 = kvh * p.G + sl * 16;
-  const int slot = p.slots ? min(max(p.slots[r], 0), p.kv_rows - 1) : r;
-  const size_t tok0 = (size_t(slot) * p.KVH + kvh) * p.cap;
-  const uint32_t cap = uint32_t(p.cap);
-  const BufRsrc rk = make_rsrc(p.kw + tok0 * 32, cap * 128u);
-  const BufRsrc rv = make_rsrc(p.vw + tok0 * 32, cap * 128u);
-  // the scale/bias array this wave stages: wave 0 K scales, 1 K biases, 2 V scales, 3 V biases
-  const void* sarr = wave == 0 ? p.ks : wave == 1 ? p.kb : wave == 2 ? p.vs : p.vb;
-  const BufRsrc rsw = make_rsrc(static_cast<const uint32_t*>(sarr) + tok0, cap * 4u);
-
-  // three separate LDS objects (not one indexed array) so the compiler can tell a slot being read from the
-  // slots the direct loads are still filling, and waits only for the block it reads; ring0 is also the
-  // 32 KB join buffer after the loop
-  __shared__ __attribute__((aligned(16))) uint8_t ring0[32768];
-  __shared__ __attribute__((aligned(16))) uint8_t ring1[kBlkBytes];
-  __shared__ __attribute__((aligned(16))) uint8_t ring2[kBlkBytes];
-
-  const int b0 = clo & ~(kBlk - 1);                      // first block
-  const int nblk = (chi - 1 - b0) / kBlk + 1;            // blocks of the chunk holding row keys
-  // a block's 20 load instructions: wave w stages K codes 1 KB pieces 2w, 2w + 1, the same V pieces, and
-  // its scale/bias array (256 B).  Code chunk p = 1024 u + 16 lane: key p / 128 ... stored at 16-byte slot
-  // (lane & 7) of its key = chunk ^ (key & 7), so the global chunk read is (lane & 7) ^ (lane >> 3).
-  const uint32_t swz = uint32_t(lane >> 3) * 128u + 16u * uint32_t((lane & 7) ^ (lane >> 3));
-  auto issue = [&](int blk, uint8_t* R) {
-    const uint32_t kb = uint32_t(b0 + blk * kBlk) * 128u;
-#pragma unroll
-    for (int h = 0; h < 2; h++) {
-      const int u = 2 * wave + h;
-      lds_load16(rk, R + u * 1024, kb + uint32_t(u) * 1024u + swz);
-      lds_load16(rv, R + 8192 + u * 1024, kb + uint32_t(u) * 1024u + swz);
-    }
-    lds_load4(rsw, R + 16384 + wave * 256, uint32_t(b0 + blk * kBlk + lane) * 4u);
-  };
-
-  // the ring's first two blocks go out first; the query's loads overlap them
-  issue(0, ring0);
-  issue(min(1, nblk - 1), ring1);  // (a repeat of block 0 when there is no second one: the count in flight stays 5 + 5)
-
-  // B operands of Q K^T: qb[4g + jj] = q[head c16][64g + 16q4 + 4jj + i]
-  h4 qb[8];
-  float qs0 = 0.0f, qs1 = 0.0f;
-  {
-    const bool real = c16 < Gs;
-    const size_t qrow = (size_t(r) * p.H + head0 + (real ? c16 : 0)) * kHD;
-    float qv0[16], qv1[16];  // dims 16 q4 .. + 15 and 64 + 16 q4 .. + 15 of the lane's head
-    ldn<QDT, 16>(p.q, qrow + 16 * q4, qv0);
-    ldn<QDT, 16>(p.q, qrow + 64 + 16 * q4, qv1);
-#pragma unroll
-    for (int j = 0; j < 8; j++) {
-      _Float16 t[4];
-#pragma unroll
-      for (int i = 0; i < 4; i++) {
-        t[i] = _Float16(real ? (j < 4 ? qv0[4 * j + i] : qv1[4 * (j - 4) + i]) : 0.0f);
-        (j < 4 ? qs0 : qs1) += float(t[i]);
-      }
-      qb[j] = h4{t[0], t[1], t[2], t[3]};
-    }
-  }
-  qs0 += __shfl_xor(qs0, 16);
-  qs0 += __shfl_xor(qs0, 32);
-  qs1 += __shfl_xor(qs1, 16);
-  qs1 += __shfl_xor(qs1, 32);
-  const float C = p.scale_log2;
-  const float zc0 = 1024.0f * qs0 * C, zc1 = 1024.0f * qs1 * C, qc0 = qs0 * C, qc1 = qs1 * C;
-
-  float m_run = -INFINITY, l_acc = 0.0f, wb0 = 0.0f, wb1 = 0.0f;
-  f4 O[8];
-#pragma unroll
-  for (int ii = 0; ii < 8; ii++) O[ii] = f4{0.0f, 0.0f, 0.0f, 0.0f};
-
-  // this wave's tile of a block: keys tb .. tb + 15 with tb = block + 16 wave
-  const int kt = 16 * wave + c16;               // A-operand key within the block
-  const int ks4 = 16 * wave + 4 * q4;           // first of the lane's 4 S/P keys within the block
-  auto compute = [&](int tb, const uint8_t* B, auto masked) {
-    constexpr bool MASKED = decltype(masked)::value;
-    const u4 ka = *reinterpret_cast<const u4*>(B + kt * 128 + 16 * ((q4) ^ (kt & 7)));
-    const u4 kc = *reinterpret_cast<const u4*>(B + kt * 128 + 16 * ((4 + q4) ^ (kt & 7)));
-    const u4 ksc = *reinterpret_cast<const u4*>(B + 16384 + 4 * ks4);
-    const u4 kbi = *reinterpret_cast<const u4*>(B + 16640 + 4 * ks4);
-    const u4 vsc = *reinterpret_cast<const u4*>(B + 16896 + 4 * ks4);
-    const u4 vbi = *reinterpret_cast<const u4*>(B + 17152 + 4 * ks4);
-    uint32_t vd[8];
-#pragma unroll
-    for (int k = 0; k < 4; k++) {
-      const int t = ks4 + k;
-#pragma unroll
-      for (int g = 0; g < 2; g++)
-        vd[2 * k + g] = *reinterpret_cast<const uint32_t*>(B + 8192 + t * 128 + 16 * ((4 * g + (c16 >> 2)) ^ (t & 7)) +
-                                                           4 * (c16 & 3));
-    }
-    f4 a0 = f4{0.0f, 0.0f, 0.0f, 0.0f}, a1 = a0;
-    a0 = mfma16(codes4_to_h4(ka.x), qb[0], a0);
-    a1 = mfma16(codes4_to_h4(kc.x), qb[4], a1);
-    a0 = mfma16(codes4_to_h4(ka.y), qb[1], a0);
-    a1 = mfma16(codes4_to_h4(kc.y), qb[5], a1);
-    a0 = mfma16(codes4_to_h4(ka.z), qb[2], a0);
-    a1 = mfma16(codes4_to_h4(kc.z), qb[6], a1);
-    a0 = mfma16(codes4_to_h4(ka.w), qb[3], a0);
-    a1 = mfma16(codes4_to_h4(kc.w), qb[7], a1);
-    h4 bv[8];
-#pragma unroll
-    for (int g = 0; g < 2; g++) {
-      const uint32_t x01 = __builtin_amdgcn_perm(vd[2 + g], vd[g], 0x05010400u);
-      const uint32_t y01 = __builtin_amdgcn_perm(vd[2 + g], vd[g], 0x07030602u);
-      const uint32_t x23 = __builtin_amdgcn_perm(vd[6 + g], vd[4 + g], 0x05010400u);
-      const uint32_t y23 = __builtin_amdgcn_perm(vd[6 + g], vd[4 + g], 0x07030602u);
-      bv[4 * g + 0] = pack_h4(codes_to_h2(x01, 0x00050004u), codes_to_h2(x23, 0x00050004u));
-      bv[4 * g + 1] = pack_h4(codes_to_h2(x01, 0x00070006u), codes_to_h2(x23, 0x00070006u));
-      bv[4 * g + 2] = pack_h4(codes_to_h2(y01, 0x00050004u), codes_to_h2(y23, 0x00050004u));
-      bv[4 * g + 3] = pack_h4(codes_to_h2(y01, 0x00070006u), codes_to_h2(y23, 0x00070006u));
-    }
-    const uint32_t kscw[4] = {ksc.x, ksc.y, ksc.z, ksc.w}, kbiw[4] = {kbi.x, kbi.y, kbi.z, kbi.w};
-    const uint32_t vscw[4] = {vsc.x, vsc.y, vsc.z, vsc.w}, vbiw[4] = {vbi.x, vbi.y, vbi.z, vbi.w};
-    float s[4];
-    bool valid[4];
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-      const float u0 = __builtin_fmaf(a0[i], C, -zc0), u1 = __builtin_fmaf(a1[i], C, -zc1);
-      float v = hpart<SDT>(kscw[i], 0) * u0;
-      v = __builtin_fmaf(hpart<SDT>(kscw[i], 1), u1, v);
-      v = __builtin_fmaf(hpart<SDT>(kbiw[i], 0), qc0, v);
-      v = __builtin_fmaf(hpart<SDT>(kbiw[i], 1), qc1, v);
-      if constexpr (MASKED) {
-        const int t = tb + 4 * q4 + i;
-        valid[i] = t >= clo && t < chi;
-        s[i] = valid[i] ? v : -INFINITY;
-      } else {
-        valid[i] = true;
-        s[i] = v;
-      }
-    }
-    float tmax = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
-    const bool need = tmax > m_run + kRescaleThr;
-    if (__any(need)) {
-      const float corr = need ? (m_run == -INFINITY ? 0.0f : fast_exp2(m_run - tmax)) : 1.0f;
-      if (need) m_run = tmax;
-      l_acc *= corr;
-      wb0 *= corr;
-      wb1 *= corr;
-#pragma unroll
-      for (int i = 0; i < 4; i++) {
-        const float ci = __shfl(corr, 4 * q4 + i);
-#pragma unroll
-        for (int ii = 0; ii < 8; ii++) O[ii][i] *= ci;
-      }
-    }
-    float w0[4], w1[4];
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-      float pr = fast_exp2(s[i] - m_run);
-      float x0 = pr * hpart<SDT>(vscw[i], 0), x1 = pr * hpart<SDT>(vscw[i], 1);
-      float y0 = pr * hpart<SDT>(vbiw[i], 0), y1 = pr * hpart<SDT>(vbiw[i], 1);
-      if constexpr (MASKED) {
-        pr = valid[i] ? pr : 0.0f;
-        x0 = valid[i] ? x0 : 0.0f;
-        x1 = valid[i] ? x1 : 0.0f;
-        y0 = valid[i] ? y0 : 0.0f;
-        y1 = valid[i] ? y1 : 0.0f;
-      }
-      l_acc += pr;
-      w0[i] = x0;
-      w1[i] = x1;
-      wb0 += __builtin_fmaf(-1024.0f, x0, y0);
-      wb1 += __builtin_fmaf(-1024.0f, x1, y1);
-    }
-    uint32_t h0a, l0a, h0b, l0b, h1a, l1a, h1b, l1b;
-    split_h2(w0[0], w0[1], h0a, l0a);
-    split_h2(w0[2], w0[3], h0b, l0b);
-    split_h2(w1[0], w1[1], h1a, l1a);
-    split_h2(w1[2], w1[3], h1b, l1b);
-    const h4 A0h = pack_h4(h0a, h0b), A0l = pack_h4(l0a, l0b);
-    const h4 A1h = pack_h4(h1a, h1b), A1l = pack_h4(l1a, l1b);
-#pragma unroll
-    for (int jj = 0; jj < 4; jj++) {
-      O[jj] = mfma16(A0h, bv[jj], O[jj]);
-      O[4 + jj] = mfma16(A1h, bv[4 + jj], O[4 + jj]);
-    }
-#pragma unroll
-    for (int jj = 0; jj < 4; jj++) {
-      O[jj] = mfma16(A0l, bv[jj], O[jj]);
-      O[4 + jj] = mfma16(A1l, bv[4 + jj], O[4 + jj]);
-    }
-  };
-
-  // block i is read from cur while block i + 2 is loaded into nxt (the slot block i - 1 used)
-  auto step = [&](int i, const uint8_t* cur, uint8_t* nxt) {
-    // own loads of block i done (block i + 1's five remain in flight), then everyone's.  A bare s_barrier:
-    // __syncthreads()'s release fence would wait for every load still filling the ring.  The acquire fence
-    // keeps this step's LDS reads below the barrier.
-    __builtin_amdgcn_s_waitcnt(0x0F75);  // vmcnt(5), expcnt/lgkmcnt untouched
-    __builtin_amdgcn_s_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-    issue(min(i + 2, nblk - 1), nxt);
-    const int tb = b0 + i * kBlk + 16 * wave;
-    if (tb + 16 > clo && tb < chi) {
-      if (tb >= clo && tb + 16 <= chi) compute(tb, cur, std::false_type{});
-      else compute(tb, cur, std::true_type{});
-    }
-  };
-  for (int i = 0; i < nblk; i += kRing) {
-    step(i, ring0, ring2);
-    if (i + 1 >= nblk) break;
-    step(i + 1, ring1, ring0);
-    if (i + 2 >= nblk) break;
-    step(i + 2, ring2, ring1);
-  }
-  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): no load into the ring outlives the loop
-  __syncthreads();
-
-  // ---- join the 4 waves in LDS (reusing the ring), one part per (row, head, chunk)
-  l_acc += __shfl_xor(l_acc, 16);
-  l_acc += __shfl_xor(l_acc, 32);
-  wb0 += __shfl_xor(wb0, 16);
-  wb0 += __shfl_xor(wb0, 32);
-  wb1 += __shfl_xor(wb1, 16);
-  wb1 += __shfl_xor(wb1, 32);
-  __shared__ float s_m[kWaves][16], s_l[kWaves][16];
-  float (&s_o)[kWaves][16][kHD] = *reinterpret_cast<float (*)[kWaves][16][kHD]>(ring0);
-  if (q4 == 0) {
-    s_m[wave][c16] = m_run;
-    s_l[wave][c16] = l_acc;
-  }
-#pragma unroll
-  for (int i = 0; i < 4; i++) {
-    const float b0v = __shfl(wb0, 4 * q4 + i), b1v = __shfl(wb1, 4 * q4 + i);
-#pragma unroll
-    for (int ii = 0; ii < 8; ii++) s_o[wave][4 * q4 + i][64 * (ii >> 2) + 4 * c16 + (ii & 3)] = O[ii][i] + (ii < 4 ? b0v : b1v);
   }
   __syncthreads();
   join_waves(p, s_m, s_l, s_o, Gs, r, head0, c);
@@ -1007,13 +766,16 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void
       qc1[e] = qs1 * C;
     }
 
-    // softmax state of head 4 e + n
-    float m_run[HG], l_acc[HG], wb0[HG], wb1[HG];
+    // softmax state of head 4 e + n: lazy running max, the reference the weights are taken against (m - pE), sums;
+    // pE is the wave-uniform prescale exponent of the V weights (lcl_common.h) and pthr the least V-scale magnitude
+    // that needs it lowered
+    float m_run[HG], mref[HG], l_acc[HG], wb0[HG], wb1[HG];
 #pragma unroll
     for (int e = 0; e < HG; e++) {
-      m_run[e] = -INFINITY;
+      m_run[e] = mref[e] = -INFINITY;
       l_acc[e] = wb0[e] = wb1[e] = 0.0f;
     }
+    int pE = kPreInit, pthr = pre_thr<SDT>(kPreInit);
     f4 O[8];
 #pragma unroll
     for (int ii = 0; ii < 8; ii++) O[ii] = f4{0.0f, 0.0f, 0.0f, 0.0f};
@@ -1103,12 +865,29 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void
         need[e] = x > m_run[e] + kRescaleThr;
         any_need = any_need || need[e];
       }
-      if (__any(any_need)) {
+      // largest |V scale| of this lane's valid keys (both groups): a scale at or above pthr needs pE lowered
+      uint32_t vmag = 0;
+  #pragma unroll
+      for (int m = 0; m < 4; m++) vmag = mag_max2(vmag, valid[m] ? vscw[m] : 0u);
+      vmag = mag_fold(vmag);
+      const bool needE = int(vmag) >= pthr;
+      if (__any(any_need || needE)) {
+        if (__any(needE)) {  // the tile's largest scale (lanes 4 b .. 4 b + 3 hold the same keys)
+          uint32_t x = vmag;
+          x = max(x, uint32_t(__shfl_xor(int(x), 4)));
+          x = max(x, uint32_t(__shfl_xor(int(x), 8)));
+          x = max(x, uint32_t(__shfl_xor(int(x), 16)));
+          x = max(x, uint32_t(__shfl_xor(int(x), 32)));
+          pE = min(pE, 9 - scale_exp<SDT>(uint32_t(uni(int(x)))));
+          pthr = pre_thr<SDT>(pE);
+        }
         float corr[HG];
   #pragma unroll
         for (int e = 0; e < HG; e++) {
-          corr[e] = need[e] ? (m_run[e] == -INFINITY ? 0.0f : fast_exp2(m_run[e] - tmax[e])) : 1.0f;
           if (need[e]) m_run[e] = tmax[e];
+          const float nref = m_run[e] - float(pE);
+          corr[e] = mref[e] == -INFINITY ? 0.0f : fast_exp2(mref[e] - nref);
+          mref[e] = nref;
           l_acc[e] *= corr[e];
           wb0[e] *= corr[e];
           wb1[e] *= corr[e];
@@ -1132,7 +911,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void
         float w0[4], w1[4];
   #pragma unroll
         for (int m = 0; m < 4; m++) {
-          float pr = fast_exp2(s[e][m] - m_run[e]);
+          float pr = fast_exp2(s[e][m] - mref[e]);
           float x0 = pr * hpart<SDT>(vscw[m], 0), x1 = pr * hpart<SDT>(vscw[m], 1);
           float y0 = pr * hpart<SDT>(vbiw[m], 0), y1 = pr * hpart<SDT>(vbiw[m], 1);
           // garbage scales of keys outside the range must not reach the sums (0 * inf)
@@ -1244,7 +1023,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void
     // lanes of quad q4 < HG write head group q4: row i of O is head 4 q4 + i
     if (q4 < HG) {
       const int e = HG == 1 ? 0 : q4;
-      const float mr = HG == 1 ? m_run[0] : (e ? m_run[HG - 1] : m_run[0]);
+      const float mr = HG == 1 ? mref[0] : (e ? mref[HG - 1] : mref[0]);
       const float la = HG == 1 ? l_acc[0] : (e ? l_acc[HG - 1] : l_acc[0]);
 #pragma unroll
       for (int i = 0; i < 4; i++) {
@@ -1322,7 +1101,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
     }
   }
 
-  float m_run = -INFINITY, l_acc = 0.0f;
+  // lazy running max and the reference p is taken against: for fp16 V, m_ref = m_run - 8, so p' = 2^8 p <= 2^14
+  // and the fp16 hi + lo split of p' keeps a normal lo down to p = 2^-11 (l and O carry the same 2^8; the partial
+  // is (m_ref, l', o')); bf16's split has no subnormal range to avoid
+  constexpr float kPPre = 8.0f;
+  float m_run = -INFINITY, mref = -INFINITY, l_acc = 0.0f;
   f4 O[8];
 #pragma unroll
   for (int ii = 0; ii < 8; ii++) O[ii] = f4{0.0f, 0.0f, 0.0f, 0.0f};
@@ -1361,8 +1144,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
     tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
     const bool need = tmax > m_run + kRescaleThr;
     if (__any(need)) {
-      const float corr = need ? (m_run == -INFINITY ? 0.0f : fast_exp2(m_run - tmax)) : 1.0f;
       if (need) m_run = tmax;
+      const float nref = KDT == DT_BF16 ? m_run : m_run - kPPre;
+      const float corr = mref == -INFINITY ? 0.0f : fast_exp2(mref - nref);
+      mref = nref;
       l_acc *= corr;
 #pragma unroll
       for (int i = 0; i < 4; i++) {
@@ -1374,7 +1159,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
     float pr[4];
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-      pr[i] = valid[i] ? fast_exp2(s[i] - m_run) : 0.0f;
+      pr[i] = valid[i] ? fast_exp2(s[i] - mref) : 0.0f;
       l_acc += pr[i];
     }
     uint32_t ha, la, hb, lb;
@@ -1426,7 +1211,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
   __shared__ float s_m[kWaves][16], s_l[kWaves][16];
   __shared__ float s_o[kWaves][16][kHD];
   if (q4 == 0) {
-    s_m[wave][c16] = m_run;
+    s_m[wave][c16] = mref;
     s_l[wave][c16] = l_acc;
   }
 #pragma unroll
@@ -1555,14 +1340,13 @@ __global__ __launch_bounds__(256) void decode_combine(CombineParams p) {
 using namespace lcl;
 
 // 8-bit pass 1 variant: the quad kernel for G <= 8 (one head group for G <= 4, two above), the register-fed one
-// otherwise.  LOCALS_AMD_DECODE=reg
-// or =lds forces the register-fed or the LDS-staged 16x16 kernel (for comparisons).
-enum { kVarAuto = 0, kVarReg = 1, kVarLds = 2 };
+// otherwise.  LOCALS_AMD_DECODE=reg forces the register-fed 16x16 kernel (for comparisons).
+enum { kVarAuto = 0, kVarReg = 1 };
 static int decode_variant() {
   static int v = -1;
   if (v < 0) {
     const char* e = getenv("LOCALS_AMD_DECODE");
-    v = !e ? kVarAuto : e[0] == 'l' ? kVarLds : e[0] == 'r' ? kVarReg : kVarAuto;
+    v = e && e[0] == 'r' ? kVarReg : kVarAuto;
   }
   return v;
 }
@@ -1575,8 +1359,6 @@ static void launch_q8_t(dim3 grid, hipStream_t stream, hipEvent_t e0, hipEvent_t
     hipExtLaunchKernelGGL((qkv_pass1_q8_quad<QDT, SDT, 1>), grid, dim3(64), 0, stream, e0, e1, 0, p);
   else if (use_quad(p))
     hipExtLaunchKernelGGL((qkv_pass1_q8_quad<QDT, SDT, 2>), grid, dim3(64), 0, stream, e0, e1, 0, p);
-  else if (decode_variant() == kVarLds)
-    hipExtLaunchKernelGGL((qkv_pass1_q8_lds<QDT, SDT>), grid, dim3(256), 0, stream, e0, e1, 0, p);
   else hipExtLaunchKernelGGL((qkv_pass1_q8<QDT, SDT>), grid, dim3(256), 0, stream, e0, e1, 0, p);
 }
 

@@ -111,17 +111,48 @@ __device__ __forceinline__ f4 mfma16bf(s4 a, s4 b, f4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
 }
 
-// two floats -> packed fp16 pair, round toward zero (v_cvt_pkrtz_f16_f32)
-__device__ __forceinline__ uint32_t pkrtz(float a, float b) {
-  return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(a, b));
+// two floats -> packed fp16 pair, round to nearest even (v_cvt_pk_f16_f32)
+__device__ __forceinline__ uint32_t pkrn(float a, float b) {
+  return __builtin_bit_cast(uint32_t, h2{_Float16(a), _Float16(b)});
 }
 
-// w ~= hi + lo with hi, lo fp16 (round toward zero): |w - hi - lo| <= 2^-21 |w|
+// w ~= hi + lo with hi, lo fp16, both rounded to nearest: hi = fp16(w), lo = fp16(w - hi) (w - hi is exact in
+// fp32).  While lo is a normal fp16 (|w| >= 2^-3) |w - hi - lo| <= 2^-22 |w|; below that lo is subnormal and the
+// error is at most 2^-25 absolute, so callers scale w up to the top of fp16's range first.
 __device__ __forceinline__ void split_h2(float a, float b, uint32_t& hi, uint32_t& lo) {
-  hi = pkrtz(a, b);
+  hi = pkrn(a, b);
+  asm("" : "+v"(hi));  // convert the pair back from the packed word (otherwise each half is converted twice)
   const h2 h = __builtin_bit_cast(h2, hi);
-  lo = pkrtz(__builtin_fmaf(float(h.x), -1.0f, a), __builtin_fmaf(float(h.y), -1.0f, b));
+  lo = pkrn(a - float(h.x), b - float(h.y));
 }
+
+// ---- prescale of the V weights in the 8-bit decode kernels
+// P V multiplies A = w = p * v_scale (as split_h2's hi + lo) by B = 1024 + code.  The softmax keeps a lazy running
+// max m (a tile's scores are at most m + 6, so p = 2^(s - m) <= 2^6) and exponentiates against m_ref = m - E for a
+// wave-uniform integer E, so p' = 2^E p and w' = p' v_scale < 2^15 whenever every |v_scale| seen is below 2^e with
+// E <= 9 - e.  E starts at kPreInit and is lowered (never raised) to 9 - e of the largest |v_scale| of a tile that
+// would break the bound; l, o and the side sums all carry the same 2^E, so the partial (m_ref, l', o') has the
+// value of (m, l, o).  With E near 9 - e the weights that matter sit in fp16's normal range.
+constexpr int kPreInit = 40;
+
+// e with |x| < 2^e for the 15-bit magnitude (bits & 0x7fff) of a 16-bit scale of dtype SDT
+template <int SDT>
+__device__ __forceinline__ int scale_exp(uint32_t mag) {
+  return SDT == DT_BF16 ? int(mag >> 7) - 126 : int(mag >> 10) - 14;
+}
+// the least magnitude whose scale_exp exceeds 9 - E (a scale that needs E lowered)
+template <int SDT>
+__device__ __forceinline__ int pre_thr(int E) {
+  const int k = (SDT == DT_BF16 ? 136 : 24) - E;
+  return k <= 0 ? 0 : (k << (SDT == DT_BF16 ? 7 : 10));
+}
+typedef unsigned short us2 __attribute__((ext_vector_type(2)));
+// running max of the magnitudes of a packed pair of 16-bit scales (magnitude order = integer order of bits & 0x7fff)
+__device__ __forceinline__ uint32_t mag_max2(uint32_t acc, uint32_t w) {
+  const us2 a = __builtin_bit_cast(us2, acc), b = __builtin_bit_cast(us2, w & 0x7fff7fffu);
+  return __builtin_bit_cast(uint32_t, __builtin_elementwise_max(a, b));
+}
+__device__ __forceinline__ uint32_t mag_fold(uint32_t acc) { return max(acc & 0xffffu, acc >> 16); }
 
 // bf16 pair by truncation: hi = top 16 bits, lo = top 16 bits of the remainder
 __device__ __forceinline__ void split_bf2(float a, float b, uint32_t& hi, uint32_t& lo) {

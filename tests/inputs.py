@@ -5,6 +5,7 @@ from __future__ import annotations
 import numpy as np
 
 from oracle import quant
+from oracle.quant import from_f32, to_f32
 
 
 def rng(seed: int) -> np.random.Generator:
@@ -37,3 +38,35 @@ def to_torch(a, dev, dtype: str = "float16"):
 
 def triple_to_torch(t, dev, dtype="float16"):
     return tuple(to_torch(x, dev, dtype) for x in t)
+
+
+def peaked_inputs(g: np.random.Generator, B, H, KVH, L, cap, lo, hi, scale=1 / np.sqrt(128), gap=(6.0, 14.0),
+                  n_dom=1, tail=0.5, v_offset=(0.75, 1.5), dtype="float16", HD=128):
+    """Queries and 8-bit K/V whose softmax is peaked: per (row b, kv head) a direction u shared by the group's
+    queries (q = 0.6 u + 0.8 N(0, 1) per head and query), ``n_dom`` keys in [lo[b], hi[b]) equal to a u with a set so
+    their logit is ``gap`` nats (U[gap]) above the rest, whose keys are N(0, tail^2) (logits ~ N(0, tail^2)), i.e.
+    one or a few dominant keys over a tail ~9..20 log2 below.  V = N(0, 0.5^2) + a per-(row, kv head, 64-dim group)
+    offset of random sign and magnitude U[v_offset], so each group's MLX scale has one sign (|max| > |min|) and the
+    rounding of the V weights cannot cancel; |V| stays below 4, where an fp16 output's own rounding (<= 2^-10) leaves
+    room under the 2e-3 bar.  Returns (q (B, H, L, HD), K triple, V triple, dominant positions (B, KVH, n_dom))."""
+    G = H // KVH
+    u = g.standard_normal((B, KVH, HD)).astype(np.float32)
+    u *= np.float32(np.sqrt(HD)) / np.linalg.norm(u, axis=-1, keepdims=True)
+    qf = (0.6 * u[:, :, None, None, :] + 0.8 * g.standard_normal((B, KVH, G, L, HD))).astype(np.float32)
+    q = from_f32(qf.reshape(B, H, L, HD), dtype)
+    qv = to_f32(q, dtype).reshape(B, KVH, G, L, HD).astype(np.float64)
+    kf = (tail * g.standard_normal((B, KVH, cap, HD))).astype(np.float32)
+    dom = np.zeros((B, KVH, n_dom), dtype=np.int64)
+    for b in range(B):
+        for h in range(KVH):
+            pos = g.choice(np.arange(lo[b], hi[b]), size=min(n_dom, hi[b] - lo[b]), replace=False)
+            dom[b, h, :len(pos)] = pos
+            # logit of a*u against the group's queries: scale * a * mean(q . u)
+            qu = float((qv[b, h] @ u[b, h]).mean()) * scale
+            for p_ in pos:
+                kf[b, h, p_] = u[b, h] * np.float32(g.uniform(*gap) / qu)
+    off = g.uniform(*v_offset, (B, KVH, 1, HD // 64)) * g.choice([-1.0, 1.0], (B, KVH, 1, HD // 64))
+    vf = (0.5 * g.standard_normal((B, KVH, cap, HD)) + np.repeat(off, 64, axis=-1)).astype(np.float32)
+    K = quant.quantize(from_f32(kf, dtype), dtype)
+    V = quant.quantize(from_f32(vf, dtype), dtype)
+    return q, K, V, dom
