@@ -7,6 +7,8 @@
  *    -1  LCL_EINVAL     bad argument (null pointer, inconsistent shape, dtype)
  *    -2  LCL_EUNSUPPORTED  shape the kernels do not implement (e.g. head_dim != 128)
  *    -3  LCL_EWORKSPACE workspace missing or smaller than *_workspace_bytes()
+ *    -4  LCL_ESCRATCH   the call needs more than the fixed scratch of the
+ *                       allocation-free entry point (LCL_NOALLOC_SCRATCH_BYTES)
  *    >0                 a hipError_t from the launch, passed through
  * All tensors are contiguous, row-major, in device memory owned by the caller.
  * dtype codes: 0 float16, 1 bfloat16, 2 float32.
@@ -25,7 +27,12 @@ extern "C" {
 #endif
 
 enum { LCL_F16 = 0, LCL_BF16 = 1, LCL_F32 = 2 };
-enum { LCL_OK = 0, LCL_EINVAL = -1, LCL_EUNSUPPORTED = -2, LCL_EWORKSPACE = -3 };
+enum { LCL_OK = 0, LCL_EINVAL = -1, LCL_EUNSUPPORTED = -2, LCL_EWORKSPACE = -3, LCL_ESCRATCH = -4 };
+
+/* Size of the device-resident scratch array behind lcl_qkv_attend_noalloc (one per GPU, held until the process
+ * ends): 32 MiB, room for the split-K parts of 16 rows x 32 heads at 64k keys (BASELINE config 2 needs 17 MB,
+ * config 3 4 MB). */
+#define LCL_NOALLOC_SCRATCH_BYTES (32u << 20)
 
 /* Bytes of split-K workspace for R query rows of H heads over `extent` keys
  * (n for lcl_qkv_attend, cap for lcl_ragged_attention) with key chunk `block`
@@ -55,6 +62,18 @@ int lcl_qkv_attend_ex(const void* q, int qdt, const uint32_t* kw, const void* ks
                       const void* vs, const void* vb, int sdt, const int32_t* start, const float* sinks, float scale,
                       int B, int H, int KVH, int head_dim, int cap, int n, int block, void* out, void* workspace,
                       size_t workspace_bytes, void* stream, void* ev_start, void* ev_stop);
+
+/* lcl_qkv_attend without a workspace argument: the same kernels, with the split-K parts in a fixed
+ * LCL_NOALLOC_SCRATCH_BYTES device array of the library instead of the caller's workspace.  No counterpart in the
+ * reference: it is for callers that cannot allocate (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc).  Calls a workspace of more than LCL_NOALLOC_SCRATCH_BYTES would need
+ * (lcl_decode_workspace_bytes(B, H, n, block)) return LCL_ESCRATCH.  It allocates nothing: the array's address is
+ * looked up once per device.  All calls on one GPU share its array, so calls that overlap on one GPU (two streams
+ * at once) race; calls ordered on one stream do not. */
+int lcl_qkv_attend_noalloc(const void* q, int qdt, const uint32_t* kw, const void* ks, const void* kb,
+                           const uint32_t* vw, const void* vs, const void* vb, int sdt, const int32_t* start,
+                           const float* sinks, float scale, int B, int H, int KVH, int head_dim, int cap, int n,
+                           int block, void* out, void* stream);
 
 /* attention.ragged_attention (locals/attention.py:200-224): row r of a packed
  * batch reads KV slot slots[r] and its first nkeys[r] keys.

@@ -17,7 +17,8 @@ LIB_PATH = os.path.join(_HERE, "liblocals_amd.so")
 
 F16, BF16, F32 = 0, 1, 2
 _DT = {torch.float16: F16, torch.bfloat16: BF16, torch.float32: F32}
-_STATUS = {-1: "invalid argument", -2: "unsupported shape", -3: "workspace too small"}
+_STATUS = {-1: "invalid argument", -2: "unsupported shape", -3: "workspace too small",
+           -4: "needs more than the allocation-free entry point's fixed scratch"}
 
 P = ctypes.c_void_p
 I = ctypes.c_int
@@ -30,6 +31,7 @@ SIGNATURES = {
     "lcl_decode_workspace_bytes": (Z, [I, I, I, I]),
     "lcl_qkv_attend": (I, [P, I, P, P, P, P, P, P, I, P, P, F, I, I, I, I, I, I, I, P, P, Z, P]),
     "lcl_qkv_attend_ex": (I, [P, I, P, P, P, P, P, P, I, P, P, F, I, I, I, I, I, I, I, P, P, Z, P, P, P]),
+    "lcl_qkv_attend_noalloc": (I, [P, I, P, P, P, P, P, P, I, P, P, F, I, I, I, I, I, I, I, P, P]),
     "lcl_ragged_attention": (I, [P, I, P, P, I, P, P, F, P, I, I, I, I, I, I, I, P, P, Z, P]),
     "lcl_ragged_attention_ex": (I, [P, I, P, P, I, P, P, F, P, I, I, I, I, I, I, I, P, P, Z, P, P, P]),
     "lcl_quantize_append": (I, [P, P, I, P, P, P, P, P, P, I, I, I, I, I, I, I, P]),

@@ -48,6 +48,7 @@
 
 #include <stdlib.h>
 
+#include <mutex>
 #include <type_traits>
 
 #include "lcl_common.h"
@@ -1460,6 +1461,58 @@ static int quad_waves(int G, int qdt, int sdt) {
   return cache[dev][v];
 }
 
+// the argument checks of lcl_qkv_attend (before anything touches the GPU)
+static int attend_args(const void* q, int qdt, const uint32_t* kw, const void* ks, const void* kb, const uint32_t* vw,
+                       const void* vs, const void* vb, int sdt, int B, int H, int KVH, int hd, int cap, int n,
+                       int block, const void* out) {
+  if (!q || !kw || !ks || !kb || !vw || !vs || !vb || !out) return -1;
+  if (hd != kHD) return -2;
+  if (B <= 0 || H <= 0 || KVH <= 0 || H % KVH || cap <= 0 || n < 0 || n > cap) return -1;
+  if (block < 0 || block % 64) return -1;
+  if ((qdt != DT_F16 && qdt != DT_BF16 && qdt != DT_F32) || (sdt != DT_F16 && sdt != DT_BF16)) return -1;
+  return 0;
+}
+
+// ---- scratch of the allocation-free decode (lcl_qkv_attend_noalloc)
+// A file-scope device array takes the place of the caller's split-K workspace.  Each GPU the library runs on holds
+// its own copy at its own address until the process ends.  On the host, `scratch` names a host-side stand-in, not
+// device memory: host code only ever uses the per-device address hipGetSymbolAddress returns (looked up once per
+// device, with that device current).  Every call on a GPU shares that GPU's array; pass 1 writes every part pass 2
+// reads (empty ones included), so nothing in it needs clearing, and calls that overlap on one GPU race.
+constexpr size_t kScratchBytes = size_t(LCL_NOALLOC_SCRATCH_BYTES);
+static_assert(kScratchBytes % 256 == 0, "scratch size");
+static __device__ __align__(256) float scratch[kScratchBytes / sizeof(float)];
+
+constexpr int kMaxDevices = 64;
+static void* g_scratch[kMaxDevices];
+static std::mutex g_scratch_mu;
+
+// the scratch address on device dev (0 = ok, else a hipError_t)
+static int scratch_on(int dev, void** out) {
+  if (dev < 0 || dev >= kMaxDevices) return int(hipErrorInvalidDevice);
+  void* p = __atomic_load_n(&g_scratch[dev], __ATOMIC_ACQUIRE);
+  if (!p) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    p = g_scratch[dev];
+    if (!p) {
+      int cur = -1;
+      hipError_t e = hipGetDevice(&cur);
+      if (e != hipSuccess) return int(e);
+      if (cur != dev && (e = hipSetDevice(dev)) != hipSuccess) return int(e);
+      e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+      if (cur != dev) {
+        const hipError_t e2 = hipSetDevice(cur);
+        if (e == hipSuccess) e = e2;
+      }
+      if (e != hipSuccess) return int(e);
+      if (!p) return int(hipErrorInvalidSymbol);
+      __atomic_store_n(&g_scratch[dev], p, __ATOMIC_RELEASE);
+    }
+  }
+  *out = p;
+  return 0;
+}
+
 extern "C" {
 
 size_t lcl_decode_workspace_bytes(int R, int H, int extent, int block) {
@@ -1481,11 +1534,7 @@ int lcl_qkv_attend_ex(const void* q, int qdt, const uint32_t* kw, const void* ks
                       int B, int H, int KVH, int hd, int cap, int n, int block, void* out, void* workspace,
                       size_t workspace_bytes, void* stream_, void* ev_start, void* ev_stop) {
   hipStream_t stream = static_cast<hipStream_t>(stream_);
-  if (!q || !kw || !ks || !kb || !vw || !vs || !vb || !out) return -1;
-  if (hd != kHD) return -2;
-  if (B <= 0 || H <= 0 || KVH <= 0 || H % KVH || cap <= 0 || n < 0 || n > cap) return -1;
-  if (block < 0 || block % 64) return -1;
-  if ((qdt != DT_F16 && qdt != DT_BF16 && qdt != DT_F32) || (sdt != DT_F16 && sdt != DT_BF16)) return -1;
+  if (const int rc = attend_args(q, qdt, kw, ks, kb, vw, vs, vb, sdt, B, H, KVH, hd, cap, n, block, out)) return rc;
   const int chunk = pick_chunk(block, n);
   DecodeParams p{};
   p.G = H / KVH;
@@ -1523,6 +1572,22 @@ int lcl_qkv_attend_ex(const void* q, int qdt, const uint32_t* kw, const void* ks
   c.quad = quad; c.R = B; c.KVH = KVH; c.G = p.G; c.qwaves = p.qwaves; c.qmint = p.qmint;
   hipLaunchKernelGGL(decode_combine, dim3(B * H, comb_slices(B * H)), dim3(256), 0, stream, c);
   return int(hipGetLastError());
+}
+
+int lcl_qkv_attend_noalloc(const void* q, int qdt, const uint32_t* kw, const void* ks, const void* kb,
+                           const uint32_t* vw, const void* vs, const void* vb, int sdt, const int32_t* start,
+                           const float* sinks, float scale, int B, int H, int KVH, int hd, int cap, int n, int block,
+                           void* out, void* stream_) {
+  if (const int rc = attend_args(q, qdt, kw, ks, kb, vw, vs, vb, sdt, B, H, KVH, hd, cap, n, block, out)) return rc;
+  if (lcl_decode_workspace_bytes(B, H, n, block) > kScratchBytes) return LCL_ESCRATCH;
+  hipStream_t stream = static_cast<hipStream_t>(stream_);
+  int dev = 0;
+  const hipError_t e = stream ? hipStreamGetDevice(stream, &dev) : hipGetDevice(&dev);
+  if (e != hipSuccess) return int(e);
+  void* ws = nullptr;
+  if (const int rc = scratch_on(dev, &ws)) return rc;
+  return lcl_qkv_attend_ex(q, qdt, kw, ks, kb, vw, vs, vb, sdt, start, sinks, scale, B, H, KVH, hd, cap, n, block,
+                           out, ws, kScratchBytes, stream_, nullptr, nullptr);
 }
 
 int lcl_ragged_attention(const void* q, int qdt, const void* keys, const void* values, int kvdt, const int32_t* slots,

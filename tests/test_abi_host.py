@@ -59,6 +59,15 @@ def test_entry_points_reject_bad_arguments_without_a_gpu():
     rc = lib.lcl_qkv_attend(one, 0, one, one, one, one, one, one, 0, None, None, 0.1, 1, 8, 2, 128, 256, 10, 0,
                             one, None, 0, None)
     assert rc == -3
+    # the allocation-free decode checks its arguments as lcl_qkv_attend does, and refuses a call whose split-K parts
+    # would not fit its fixed scratch (64 rows x 64 heads over 128k keys need ~550 MB), before touching the GPU
+    rc = lib.lcl_qkv_attend_noalloc(None, 0, one, one, one, one, one, one, 0, None, None, 0.1, 1, 8, 2, 128, 256, 10,
+                                    0, one, None)
+    assert rc == -1
+    assert lib.lcl_decode_workspace_bytes(64, 64, 131072, 0) > (32 << 20)
+    rc = lib.lcl_qkv_attend_noalloc(one, 0, one, one, one, one, one, one, 0, None, None, 0.1, 64, 64, 8, 128, 131072,
+                                    131072, 0, one, None)
+    assert rc == -4
     rc = lib.lcl_quantize_append(one, None, 0, one, one, one, None, None, None, 1, 1, 4, 100, 8, 0, 0, None)
     assert rc == -1  # D not a multiple of 64
     # parts a (row, head): max(key chunks of 512, stream-K slots: ceil(16 tiles / 8 a wave) + 1) = 3
