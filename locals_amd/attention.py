@@ -1,9 +1,10 @@
-"""Ragged batch decode attention: one launch for all rows of all requests -- drop-in for ``locals/attention.py``.
+"""``ragged_attention`` on the MI355X: decode attention over 16-bit K/V for a packed batch in a single launch.
 
-Row r of the packed batch belongs to KV slot ``slots[r]`` and may see the first ``nkeys[r]`` keys of that slot
-(its prefix plus the earlier new tokens of its own segment, which gives the causal mask for multi-token segments);
-K/V live in slot-major buffers (n_slots, n_kv_heads, cap, D) (locals/attention.py:1-8).  Backed by
-``lcl_ragged_attention`` (split-K flash decode on MFMA over fp16/bf16 K/V).
+The call surface is the reference's (locals/attention.py:200-224).  Each query row names the KV slot it reads
+(``slots``) and how many of that slot's leading keys it sees (``nkeys``); a multi-token segment gets its causal
+mask by giving each of its rows one more key than the row before.  K and V are slot-major buffers
+(n_slots, Hkv, cap, D).  The work runs in ``lcl_ragged_attention``: a split-K pass 1 on MFMA and a log-sum-exp
+join.
 """
 
 from __future__ import annotations
@@ -18,8 +19,10 @@ BLOCK = 0  # keys a pass-1 workgroup reads (a multiple of 64); 0: the library's 
 
 def ragged_attention(q: torch.Tensor, keys: torch.Tensor, values: torch.Tensor, slots: torch.Tensor,
                      nkeys: torch.Tensor, scale) -> torch.Tensor:
-    """q: (R, H, D); keys/values: (n_slots, Hkv, cap, D); slots/nkeys: (R,) int32; scale: (1,) float32 tensor or a
-    float.  Returns (R, H, D) (locals/attention.py:200-224).  A row with no keys gives 0."""
+    """Attention of R query rows (q (R, H, D)) over slot-major K/V (n_slots, Hkv, cap, D): row r reads slot
+    ``slots[r]``, keys [0, ``nkeys[r]``).  ``scale`` is a float or a (1,) float32 tensor (a GPU tensor is read on
+    the device).  Returns (R, H, D) in q's dtype; a row whose ``nkeys`` is 0 comes back as zeros
+    (locals/attention.py:200-224)."""
     if q.dim() != 3 or keys.dim() != 4 or values.shape != keys.shape:
         raise ValueError("q (R, H, D), keys/values (n_slots, Hkv, cap, D) expected")
     R, H, D = q.shape

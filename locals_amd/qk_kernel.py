@@ -26,9 +26,9 @@ HEAD_DIMS = (128, 256, 512)  # the head sizes the kernel is built for
 
 
 def fits(attn, qkv: torch.Tensor) -> bool:
-    """Whether qk_norm_rope computes this layer (locals/qk_kernel.py:74-82): a 16-bit activation, a head size the
-    kernel is built for (a multiple of 128: 128, 256 or 512), both norm weights in the activation's dtype, the same
-    norm eps for q and k, and RoPE (where the layer has it) rotating whole heads by halves at scale 1."""
+    """True when the fused kernel can take this layer (the predicate of locals/qk_kernel.py:74-82): fp16 or bf16
+    activations with norm weights of the same dtype, a head size the kernel handles (``HEAD_DIMS``), one eps shared
+    by the q and k norms, and either no RoPE or a non-traditional RoPE of unit scale over the full head."""
     hd = attn.head_dim
     rope = attn.rope
     return (USE_QK_KERNEL and qkv.dtype in (torch.bfloat16, torch.float16) and hd in HEAD_DIMS
@@ -66,9 +66,10 @@ def _common(qkv: torch.Tensor, attn):
 
 
 def qk_norm_rope(qkv: torch.Tensor, attn, offset):
-    """(q, k, v) of ``qkv`` (B, L, (H + 2 KV) * HD): q and k normed and, where ``attn.rope``, rotated to positions
-    ``offset`` + 0..L-1 (an int, or one per row as a batch cache's ``offset``); q (B, H, L, HD), k and v
-    (B, KV, L, HD), v its own array (locals/qk_kernel.py:85-109)."""
+    """Split the fused projection ``qkv`` (B, L, (H + 2 KV) * HD) into q (B, H, L, HD), k and v (B, KV, L, HD).
+    q and k get their per-head RMS norm and, when the layer has ``attn.rope``, RoPE at positions ``offset + l``;
+    ``offset`` is an int or a per-row tensor (a batch cache's ``offset``).  v is a fresh tensor, not a view of
+    ``qkv`` (locals/qk_kernel.py:85-109)."""
     B, L, H, KV, HD, dev, x, qw, kw, eps, lb, rope = _common(qkv, attn)
     offs, per_row = _offsets(offset, B, dev)
     q = torch.empty((B, H, L, HD), dtype=qkv.dtype, device=dev)

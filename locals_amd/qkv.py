@@ -54,11 +54,13 @@ def workspace_bytes(R: int, H: int, extent: int, block: int = 0) -> int:
 
 def attend(q: torch.Tensor, keys, values, n: int, sinks: Optional[torch.Tensor], scale: float,
            start: Optional[torch.Tensor]) -> torch.Tensor:
-    """One query per row against 8-bit keys and values (locals/qkv.py:213-249).
+    """Decode attention of a single query token per row over an 8-bit cache (locals/qkv.py:213-249).
 
-    ``q`` (B, H, 1, HD) with HD = 128; ``keys``/``values`` a cache's whole buffers, (words, scales, biases) of shape
-    (B, KVH, capacity, ...), read in place; positions ``start[b]`` to ``n`` are row b's.  Softmax over those keys and
-    the head's sink (``sinks`` (H,), any float dtype, or None for no sink).  Returns (B, H, 1, HD) in q's dtype.
+    ``q`` is (B, H, 1, 128).  ``keys`` and ``values`` are the cache's full (words, scales, biases) buffers,
+    (B, KVH, capacity, ...); they are consumed where they lie, without copying out the live part.  Row b uses
+    buffer positions ``start[b]`` up to ``n`` (``start`` None means 0).  Each head's softmax also counts its sink
+    logit ``sinks[h]`` in the denominator (``sinks`` (H,) of any float dtype, or None).  The result is
+    (B, H, 1, 128) in q's dtype.
     """
     if q.dim() != 4 or q.shape[2] != 1:
         raise ValueError("attend takes one query a row: q (B, H, 1, HD)")
@@ -181,8 +183,9 @@ def quantized(cache) -> bool:
 
 
 def attention(q, k, v, cache, scale: float, mask, sinks) -> torch.Tensor:
-    """A layer's attention through a quantized cache (locals/qkv.py:260-272): stores ``k``/``v`` (B, KVH, L, HD),
-    then one query a row through ``attend``, a prompt or a tree (several) through the masked 8-bit kernel."""
+    """Append this step's ``k``/``v`` (B, KVH, L, HD) to the 8-bit ``cache``, then attend (locals/qkv.py:260-272):
+    single-token decode (L == 1, head size 128) goes to ``attend``; a prompt chunk, span or tree (L > 1) goes to the
+    masked kernel, which reads the 8-bit cache without a dequantized copy."""
     cache.update_and_fetch(k, v)
     return attend_cache(q, cache, scale, mask, sinks)
 
@@ -199,7 +202,8 @@ def attend_cache(q, cache, scale: float, mask, sinks) -> torch.Tensor:
         return attend(q, cache.keys, cache.values, n, sinks, scale, start)
     from .fuse import attend_few_q8
 
-    return attend_few_q8(q, keys, values, scale, mask, sinks)
+    # the prompt branch hands the sinks over in the queries' dtype (locals/qkv.py:272: sinks.astype(q.dtype))
+    return attend_few_q8(q, keys, values, scale, mask, None if sinks is None else sinks.to(q.dtype))
 
 
 def _zeros_like_shape(B, H, n, D, dtype, device, empty=False):
@@ -250,23 +254,33 @@ def dynamic_roll(a: torch.Tensor, shifts: torch.Tensor, axis: int = 2) -> torch.
     return torch.gather(a, axis, idx)
 
 
-def _grow(cache, B: int, H: int, prev: int, S: int, D: int, dtype, device) -> None:
-    """Make ``cache.keys``/``values`` hold prev + S positions: new zeroed buffers of whole ``step``s, the first prev
-    positions copied over (locals/qkv.py:309-319)."""
+def _grow(cache, B: int, H: int, prev: int, S: int, D: int, dtype, device, keep_aligned: bool = False) -> None:
+    """Room for S positions at ``prev``: when the buffers are missing or too short, the kept positions are followed
+    by ``ceil(S / step) * step`` zeroed ones.  The batch cache keeps exactly ``prev`` (locals/qkv.py:311-319), so its
+    capacity becomes prev + ceil(S / step) * step; the one-request cache follows mlx-lm's QuantizedKVCache
+    (``keep_aligned``): it drops the positions past ``prev`` only when ``prev`` is not a multiple of ``step``, and
+    otherwise keeps its whole buffer."""
     if cache.keys is not None and prev + S <= cache.keys[0].shape[2]:
         return
-    cap = (prev + S + cache.step - 1) // cache.step * cache.step
-    nk = _zeros(B, H, cap, D, dtype, device)
-    nv = _zeros(B, H, cap, D, dtype, device)
-    if cache.keys is not None:
+    grow = (S + cache.step - 1) // cache.step * cache.step
+    if cache.keys is None:
+        keep = 0
+    elif keep_aligned and prev % cache.step == 0:
+        keep = cache.keys[0].shape[2]
+    else:
+        keep = prev
+    nk = _zeros(B, H, keep + grow, D, dtype, device)
+    nv = _zeros(B, H, keep + grow, D, dtype, device)
+    if keep:
         for a, z in zip(cache.keys + cache.values, nk + nv):
-            z[..., :prev, :] = a[..., :prev, :]
+            z[..., :keep, :] = a[..., :keep, :]
     cache.keys, cache.values = nk, nv
 
 
 class QuantizedKVCache8:
-    """mlx-lm's QuantizedKVCache in 8 bits (locals/qkv.py:284-292): one request's (words, scales, biases) buffers
-    growing by ``step`` positions; ``merge`` makes a BatchQuantizedKVCache."""
+    """Cache of one request in 8-bit triples, with mlx-lm's QuantizedKVCache bookkeeping at bits 8, group 64
+    (locals/qkv.py:284-292).  Buffers grow in units of ``step`` positions; ``merge`` of several of these builds a
+    BatchQuantizedKVCache."""
 
     step = 256
     bits, group_size = BITS, GROUP
@@ -278,7 +292,7 @@ class QuantizedKVCache8:
     def _reserve(self, B: int, H: int, S: int, D: int, dtype, device) -> int:
         """Grow the buffers to hold S more positions and advance the offset; returns where the S positions go."""
         prev = self.offset
-        _grow(self, B, H, prev, S, D, dtype, device)
+        _grow(self, B, H, prev, S, D, dtype, device, keep_aligned=True)
         self.offset += S
         return prev
 
@@ -335,9 +349,10 @@ class QuantizedKVCache8:
 
 
 class BatchQuantizedKVCache:
-    """mlx-lm's BatchKVCache (left-padded rows, one buffer index ``_idx``, ``offset`` each row's position) with the
-    keys and values as 8-bit (words, scales, biases) triples (locals/qkv.py:295-452).  ``left_padding`` and
-    ``offset`` are int32 device tensors; ``_idx`` is a host int.  Capacities grow by whole ``step``s."""
+    """Cache of a batch of requests in 8-bit triples (locals/qkv.py:295-452), kept as mlx-lm's BatchKVCache keeps
+    its rows: rows are aligned on the right with ``left_padding`` blank positions in front, all rows share the write
+    position ``_idx`` (a host int), and ``offset`` (int32 device tensor, like ``left_padding``) is each row's own
+    token count.  Growth appends whole ``step``s after the used positions."""
 
     step = 256
     bits, group_size = BITS, GROUP

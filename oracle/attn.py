@@ -17,7 +17,7 @@ from __future__ import annotations
 
 import numpy as np
 
-from .quant import dequantize, to_f32
+from .quant import dequantize, from_f32, to_f32
 
 
 def _f64(x, dtype="float16"):
@@ -169,6 +169,14 @@ def sdpa_q8(q, keys, values, scale: float, mask=None, sinks=None, n: int | None 
         kd, vd = kd[:, :, :n], vd[:, :, :n]
     sk = None if sinks is None else _f64(sinks, dtype)
     return sdpa(_f64(q, dtype), kd, vd, scale, mask, sk, dtype="float64")
+
+
+def attention_prompt(q, keys, values, scale: float, mask, sinks_f32, n: int, dtype: str = "float16"):
+    """``qkv.attention``'s prompt branch (locals/qkv.py:270-272) after the store: the sinks, given as float32 values
+    (a model's parameter), are cast to the queries' dtype (``sinks.astype(q.dtype)``) before ``attend_few`` over the
+    dequantized cache; the rest is ``sdpa_q8``."""
+    sk = None if sinks_f32 is None else from_f32(np.asarray(sinks_f32, dtype=np.float32), dtype)
+    return sdpa_q8(q, keys, values, scale, mask, sk, n=n, dtype=dtype)
 
 
 def ragged_attention(q, keys, values, slots, nkeys, scale) -> np.ndarray:

@@ -155,3 +155,84 @@ def test_batch_cache_merge_extend_filter_extract_on_host():
     for a, x in zip(b.keys, c1.keys):
         assert torch.equal(a[0, :, :20], x[0, :, :20])
     assert b.nbytes == sum(a.numel() * a.element_size() for a in b.keys + b.values)
+
+
+def test_batch_cache_growth_follows_the_reference_rule():
+    """BatchQuantizedKVCache grows to prev + ceil(S / 256) * 256 positions, keeping exactly the first prev
+    (locals/qkv.py:311-319: concatenate(a[..., :prev, :], zeros(ceil(S / step) * step))).  Capacities below are
+    worked out by hand from that rule; nbytes is 272 B a position and kv head (128 + 4 + 4 for K and for V)."""
+    from locals_amd import qkv
+
+    def step(c, S):
+        c._reserve(c.left_padding.numel(), 2, S, 128, torch.float16, torch.device("cpu"))
+        return c.keys[0].shape[2]
+
+    # merge (700 and 300 keys: buffers of exactly 700) then decode steps
+    c1, c2 = qkv.QuantizedKVCache8(), qkv.QuantizedKVCache8()
+    c1.keys, c1.values, c1.offset = _filled(1, 2, 768, 1), _filled(1, 2, 768, 2), 700
+    c2.keys, c2.values, c2.offset = _filled(1, 2, 512, 3), _filled(1, 2, 512, 4), 300
+    b = qkv.QuantizedKVCache8.merge([c1, c2])
+    assert b.keys[0].shape[2] == 700
+    assert step(b, 1) == 956  # 700 + 256
+    assert step(b, 255) == 956  # 956 positions used, no growth
+    assert step(b, 1) == 1212  # 956 + 256
+    assert b._idx == 957 and b.offset.tolist() == [957, 557]
+    assert b.nbytes == 2 * 2 * 1212 * 272
+    keys, values, offset, lp, idx = b.state
+    assert keys[0].shape == (2, 2, 1212, 32) and keys[1].shape == (2, 2, 1212, 2) and idx == 957
+    # a prompt chunk, a step, a longer chunk
+    e = qkv.BatchQuantizedKVCache([0, 0])
+    assert step(e, 700) == 768  # 0 + 3 * 256
+    assert step(e, 1) == 768
+    assert step(e, 300) == 1213  # 701 + 2 * 256
+    # the kept positions are copied, the new ones are zero
+    e2 = qkv.BatchQuantizedKVCache([0])
+    e2.keys, e2.values, e2._idx = _filled(1, 2, 300, 7), _filled(1, 2, 300, 8), 300
+    e2.offset = torch.tensor([300], dtype=torch.int32)
+    old = [a.clone() for a in e2.keys]
+    assert step(e2, 10) == 556
+    assert all(torch.equal(a[..., :300, :], o) for a, o in zip(e2.keys, old))
+    assert not any(a[..., 300:, :].any() for a in e2.keys)
+    # extend takes the larger capacity of the two sides
+    b.extend(e)
+    assert b.keys[0].shape[2] == 1213 and b._idx == 1001
+
+
+def test_single_cache_growth_follows_mlx_lm():
+    """QuantizedKVCache8 (mlx-lm's QuantizedKVCache): grows by ceil(S / 256) * 256, dropping positions past the
+    offset first only when the offset is not a multiple of 256."""
+    from locals_amd import qkv
+
+    c = qkv.QuantizedKVCache8()
+    cpu = torch.device("cpu")
+    c._reserve(1, 2, 300, 128, torch.float16, cpu)
+    assert c.keys[0].shape[2] == 512 and c.offset == 300
+    c._reserve(1, 2, 100, 128, torch.float16, cpu)
+    assert c.keys[0].shape[2] == 512
+    c._reserve(1, 2, 200, 128, torch.float16, cpu)  # 400 % 256 != 0: keep 400, add 256
+    assert c.keys[0].shape[2] == 656 and c.offset == 600
+    c.trim(88)  # offset 512, a multiple of 256: the whole buffer is kept on the next growth
+    c._reserve(1, 2, 200, 128, torch.float16, cpu)
+    assert c.keys[0].shape[2] == 912 and c.offset == 712
+    assert c.nbytes == 2 * 912 * 272
+
+
+def test_prompt_branch_hands_sinks_over_in_the_query_dtype(monkeypatch):
+    """qkv.attention's prompt branch casts the sinks to q's dtype (locals/qkv.py:272) before the masked kernel."""
+    from locals_amd import fuse, qkv
+
+    seen = {}
+
+    def fake(q, keys, values, scale, mask, sinks):
+        seen["sinks"] = sinks
+        return q
+
+    monkeypatch.setattr(fuse, "attend_few_q8", fake)
+    c = qkv.QuantizedKVCache8()
+    c.keys, c.values, c.offset = _filled(1, 2, 256, 1), _filled(1, 2, 256, 2), 10
+    q = torch.zeros(1, 4, 3, 128, dtype=torch.bfloat16)
+    s32 = torch.tensor([0.1234567, -3.3333333, 2.0000001, 7.7777777], dtype=torch.float32)
+    qkv.attend_cache(q, c, 0.1, "causal", s32)
+    assert seen["sinks"].dtype == torch.bfloat16 and torch.equal(seen["sinks"], s32.to(torch.bfloat16))
+    qkv.attend_cache(q, c, 0.1, "causal", None)
+    assert seen["sinks"] is None

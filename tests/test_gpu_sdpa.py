@@ -258,6 +258,32 @@ def test_qkv_attention_prompt_branch(dev):
     assert np.abs(_np(out) - ref).max() <= 2e-3
 
 
+@pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
+def test_qkv_attention_prompt_branch_fp32_sinks(dev, dtype):
+    """A model's sinks are fp32 parameters; the prompt branch hands them over cast to q's dtype (locals/qkv.py:272),
+    so the output equals the call given the rounded sinks, bit for bit, and the oracle of that branch."""
+    from locals_amd import qkv
+
+    g = rng(13)
+    B, H, KVH, L0, L = 1, 8, 2, 300, 9
+    cache = qkv.QuantizedKVCache8()
+    k0, v0 = normal16(g, (B, KVH, L0, 128), dtype=dtype), normal16(g, (B, KVH, L0, 128), dtype=dtype)
+    cache.update_and_fetch(to_torch(k0, dev, dtype), to_torch(v0, dev, dtype))
+    q = normal16(g, (B, H, L, 128), dtype=dtype)
+    k1, v1 = normal16(g, (B, KVH, L, 128), dtype=dtype), normal16(g, (B, KVH, L, 128), dtype=dtype)
+    s32 = (3.0 + g.standard_normal(H)).astype(np.float32)  # sinks that carry a tenth of the softmax weight
+    qt = to_torch(q, dev, dtype)
+    out = qkv.attention(qt, to_torch(k1, dev, dtype), to_torch(v1, dev, dtype), cache, 0.0884, "causal",
+                        torch.from_numpy(s32).to(dev))
+    again = qkv.attend_cache(qt, cache, 0.0884, "causal", torch.from_numpy(s32).to(dev).to(qt.dtype))
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), again.view(torch.int16))
+    K = oq.quantize(np.concatenate([k0, k1], 2), dtype)
+    V = oq.quantize(np.concatenate([v0, v1], 2), dtype)
+    ref = oa.attention_prompt(q, K, V, 0.0884, "causal", s32, n=L0 + L, dtype=dtype)
+    assert np.abs(_np(out) - ref).max() <= _tol(ref, dtype)
+
+
 @pytest.mark.parametrize("kvdt", ["float16", "bfloat16"])
 @pytest.mark.parametrize("W", [1, 37, 129, 513, 100000])
 def test_window_16bit(dev, kvdt, W):
