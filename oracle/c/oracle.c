@@ -16,6 +16,17 @@
  *                round to nearest even).  round_mode 0 = half away from zero
  *                (roundf, Metal round), 1 = half to even (rintf).
  *
+ * orc_sdpa       MLX scaled_dot_product_attention as the reference's multi-query
+ *                variants call it (qkv.attention's prompt branch over the
+ *                dequantized cache, locals/qkv.py:270-272 -> fuse.attend_few,
+ *                locals/fuse.py:131-144; tree verification, locals/treedec.py:
+ *                56-79): K/V given as fp32 values (the caller dequantizes and
+ *                rounds them to the activation dtype), masks: causal aligned to
+ *                the last key (fuse.py:131-137), tree (prefix visible, new keys by
+ *                ancestor bits), dense, sliding window, left padding; the sink a
+ *                logit in the denominator only.  Scores are fp32 dot products;
+ *                the softmax sums and the P V accumulation are double.  OpenMP
+ *                over (row, kv head, block of 16 queries).
  * Build: oracle/Makefile (gcc -O2 -fopenmp, no fast-math: divisions stay
  * correctly rounded and nothing is contracted).
  */
@@ -152,4 +163,95 @@ int orc_attend_q8(const float *q, const uint32_t *kw, const float *ks, const flo
   free(pl);
   free(po);
   return 0;
+}
+
+/* q (B,H,L,D); k, v (B,KVH,cap,D) fp32 values; keys [0, N) of each buffer row.
+ * mask_kind 0 none, 1 causal (query i sees key j <= N - L + i), 2 tree (key
+ * j < N - L for all; key N - L + d iff bit d of tree[b*L + i]), 3 dense
+ * (dense[(b*L + i)*N + j] != 0, shared by the heads), 4 window (N - L + i -
+ * window < j <= N - L + i).  start (B,) or NULL hides keys before start[b].
+ * sinks (H,) or NULL.  out (B,H,L,D); a query with no visible key and no sink
+ * gives 0. */
+int orc_sdpa(const float *q, const float *k, const float *v, const int32_t *start, int mask_kind,
+             const uint64_t *tree, const uint8_t *dense, int window, const float *sinks, float scale, int B,
+             int H, int KVH, int L, int N, int D, int cap, float *out) {
+  if (H % KVH || N > cap || L > N || (mask_kind == 2 && L > 64) || mask_kind < 0 || mask_kind > 4) return -1;
+  const int G = H / KVH, QB = 16;
+  const int nqb = (L + QB - 1) / QB;
+  const int off = N - L;
+  int fail = 0;
+#pragma omp parallel for collapse(3) schedule(dynamic, 1)
+  for (int b = 0; b < B; b++)
+    for (int h = 0; h < KVH; h++)
+      for (int qb = 0; qb < nqb; qb++) {
+        const int i0 = qb * QB, i1 = i0 + QB < L ? i0 + QB : L;
+        const int R = (i1 - i0) * G; /* rows: (query i, head g) */
+        float *qs = malloc(sizeof(float) * (size_t)R * D); /* transposed: qs[d * R + r] */
+        float *acc = malloc(sizeof(float) * (size_t)R);
+        float *S = malloc(sizeof(float) * (size_t)R * N);
+        double *o = malloc(sizeof(double) * (size_t)R * D);
+        double *den = malloc(sizeof(double) * (size_t)R);
+        float *M = malloc(sizeof(float) * (size_t)R);
+        if (!qs || !acc || !S || !o || !den || !M) {
+#pragma omp atomic write
+          fail = 1;
+          free(qs); free(acc); free(S); free(o); free(den); free(M);
+          continue;
+        }
+        for (int i = i0; i < i1; i++)
+          for (int g = 0; g < G; g++) {
+            const int r = (i - i0) * G + g;
+            const float *src = q + (((size_t)b * H + h * G + g) * L + i) * D;
+            for (int d = 0; d < D; d++) qs[(size_t)d * R + r] = src[d];
+          }
+        const size_t kv0 = ((size_t)b * KVH + h) * cap;
+        const int s0 = start && start[b] > 0 ? start[b] : 0;
+        /* scores: key j against every row; each row's sum runs over the dims in order, the rows side by side */
+        for (int j = 0; j < N; j++) {
+          const float *kj = k + (kv0 + j) * D;
+          for (int r = 0; r < R; r++) acc[r] = 0.0f;
+          for (int d = 0; d < D; d++) {
+            const float kd = kj[d];
+            const float *qd = qs + (size_t)d * R;
+            for (int r = 0; r < R; r++) acc[r] += qd[r] * kd;
+          }
+          for (int r = 0; r < R; r++) {
+            const int i = i0 + r / G;
+            int vis = j >= s0;
+            if (mask_kind == 1) vis = vis && j <= off + i;
+            else if (mask_kind == 2) vis = vis && (j < off || ((tree[(size_t)b * L + i] >> (j - off)) & 1u));
+            else if (mask_kind == 3) vis = vis && dense[((size_t)b * L + i) * N + j];
+            else if (mask_kind == 4) vis = vis && j <= off + i && j > off + i - window;
+            S[(size_t)r * N + j] = vis ? acc[r] * scale : -INFINITY;
+          }
+        }
+        for (int r = 0; r < R; r++) {
+          const int g = r % G;
+          const float sink = sinks ? sinks[h * G + g] : -INFINITY;
+          float m = sink;
+          for (int j = 0; j < N; j++) m = fmaxf(m, S[(size_t)r * N + j]);
+          M[r] = m;
+          den[r] = (m == -INFINITY || !sinks) ? 0.0 : exp((double)sink - (double)m);
+          for (int d = 0; d < D; d++) o[(size_t)r * D + d] = 0.0;
+        }
+        for (int j = 0; j < N; j++) {
+          const float *vj = v + (kv0 + j) * D;
+          for (int r = 0; r < R; r++) {
+            const float sj = S[(size_t)r * N + j];
+            if (sj == -INFINITY) continue;
+            const double p = exp((double)sj - (double)M[r]);
+            den[r] += p;
+            double *orow = o + (size_t)r * D;
+            for (int d = 0; d < D; d++) orow[d] += p * (double)vj[d];
+          }
+        }
+        for (int i = i0; i < i1; i++)
+          for (int g = 0; g < G; g++) {
+            const int r = (i - i0) * G + g;
+            float *dst = out + (((size_t)b * H + h * G + g) * L + i) * D;
+            for (int d = 0; d < D; d++) dst[d] = den[r] > 0.0 ? (float)(o[(size_t)r * D + d] / den[r]) : 0.0f;
+          }
+        free(qs); free(acc); free(S); free(o); free(den); free(M);
+      }
+  return fail ? -2 : 0;
 }

@@ -70,3 +70,37 @@ def peaked_inputs(g: np.random.Generator, B, H, KVH, L, cap, lo, hi, scale=1 / n
     K = quant.quantize(from_f32(kf, dtype), dtype)
     V = quant.quantize(from_f32(vf, dtype), dtype)
     return q, K, V, dom
+
+
+def peaked_inputs_torch(gen, dev, B, H, KVH, L, cap, lo, hi, scale=1 / np.sqrt(128), gap=(6.0, 14.0), n_dom=1,
+                        tail=0.5, v_offset=(0.75, 1.5), HD=128):
+    """``peaked_inputs`` drawn on the GPU with a torch Generator, for full-size cases: fp16 q (B, H, L, HD) and 8-bit
+    K/V triples (B, KVH, cap, .) quantized by the library's quantize kernel (bit-exact with oracle.quant, a GPU test
+    of its own).  Same recipe: a direction u per (row, kv head) shared by its queries, ``n_dom`` keys in
+    [lo[b], hi[b]) set to a u with their logit ``gap`` nats above a N(0, tail^2) tail, V = N(0, 0.5^2) plus a
+    per-(row, kv head, group) offset of random sign."""
+    import torch
+
+    from locals_amd import qkv
+
+    G = H // KVH
+    f = dict(generator=gen, device=dev, dtype=torch.float32)
+    u = torch.randn((B, KVH, HD), **f)
+    u = u * (HD ** 0.5) / u.norm(dim=-1, keepdim=True)
+    q = (0.6 * u[:, :, None, None, :] + 0.8 * torch.randn((B, KVH, G, L, HD), **f)).to(torch.float16)
+    qu = (q.float() @ u[:, :, None, :, None]).mean(dim=(2, 3, 4)) * scale  # (B, KVH): logit of u against the queries
+    K = qkv._zeros(B, KVH, cap, HD, torch.float16, dev)
+    V = qkv._zeros(B, KVH, cap, HD, torch.float16, dev)
+    for b in range(B):  # a row at a time keeps the temporaries small
+        kf = tail * torch.randn((1, KVH, cap, HD), **f)
+        for h in range(KVH):
+            span = int(hi[b]) - int(lo[b])
+            pos = int(lo[b]) + torch.randperm(span, generator=gen, device=dev)[:n_dom]
+            a = (gap[0] + (gap[1] - gap[0]) * torch.rand((n_dom,), **f)) / qu[b, h]
+            kf[0, h, pos] = a[:, None] * u[b, h][None, :]
+        sgn = torch.where(torch.rand((1, KVH, 1, HD // 64), **f) < 0.5, -1.0, 1.0)
+        off = sgn * (v_offset[0] + (v_offset[1] - v_offset[0]) * torch.rand((1, KVH, 1, HD // 64), **f))
+        vf = 0.5 * torch.randn((1, KVH, cap, HD), **f) + off.repeat_interleave(64, dim=-1)
+        qkv.quantize_into(kf.to(torch.float16), vf.to(torch.float16), tuple(t[b:b + 1] for t in K),
+                          tuple(t[b:b + 1] for t in V), 0)
+    return q.reshape(B, H, L, HD), K, V

@@ -1,0 +1,141 @@
+"""GPU parity at the BASELINE configurations' full sizes, against the C restatements in oracle/c (pinned to the
+float64 oracle on small cases in tests/test_oracle.py), with peaked softmaxes (one dominant key over a deep tail,
+V groups with a common offset) and with the bench's N(0, 1) draws:
+
+* C3: one row, 16 / 8 heads, 245,760 keys of 8-bit K/V (split-K over ~256 waves a stream), vs the reference's
+  two-pass split-K decode restated in C (locals/qkv.py:30-87, 179-208).
+* C4: the 512-query causal prompt chunk over 16,896 8-bit keys, 32 / 8 heads, through both routes (dequantize-first
+  and the fused 8-bit kernel), vs masked SDPA restated in C over the dequantized cache (locals/qkv.py:270-272);
+  and its 15 decode rows (contexts U[2k, 16k]).
+* C5: 8 rows x 16 draft tokens in random trees (branching 1-3, depth <= 8) over 8,192 cached 8-bit keys, the
+  ancestor-only mask (locals/treedec.py:56-67), vs the same C SDPA.
+Bar: 2e-3 max-abs (fp16 outputs)."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import cbind
+from tests.inputs import peaked_inputs_torch
+
+pytestmark = pytest.mark.gpu
+
+SCALE = 1 / np.sqrt(128)
+
+
+def _host_triple(t):
+    return (t[0].cpu().numpy().view(np.uint32), t[1].cpu().numpy(), t[2].cpu().numpy())
+
+
+def _err(got, ref):
+    return float(np.abs(got.float().cpu().numpy().astype(np.float64) - np.asarray(ref, dtype=np.float64)).max())
+
+
+@pytest.mark.parametrize("peaked", [True, False])
+def test_c3_full_size(dev, peaked):
+    from locals_amd import qkv
+
+    B, H, KVH, n = 1, 16, 8, 245760
+    print(f"C3 full size peaked={peaked}", flush=True)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(31 + peaked)
+    if peaked:
+        q, K, V = peaked_inputs_torch(gen, dev, B, H, KVH, 1, n, [0], [n], scale=SCALE, n_dom=2)
+    else:
+        K = qkv._zeros(B, KVH, n, 128, torch.float16, dev)
+        V = qkv._zeros(B, KVH, n, 128, torch.float16, dev)
+        qkv.quantize_into(torch.randn((B, KVH, n, 128), generator=gen, device=dev, dtype=torch.float16),
+                          torch.randn((B, KVH, n, 128), generator=gen, device=dev, dtype=torch.float16), K, V, 0)
+        q = torch.randn((B, H, 1, 128), generator=gen, device=dev, dtype=torch.float16)
+    sinks = torch.randn((H,), generator=gen, device=dev) * 2
+    start = torch.zeros((B,), dtype=torch.int32, device=dev)
+    got = qkv.attend(q, K, V, n, sinks, SCALE, start)
+    torch.cuda.synchronize()
+    ref = cbind.attend_q8(q.cpu().numpy(), _host_triple(K), _host_triple(V), n, sinks.cpu().numpy(), SCALE,
+                          np.zeros(B, np.int32), threads=16)
+    err = _err(got, ref)
+    print(f"  C3 max |gpu - C| = {err:.3g}", flush=True)
+    assert err <= 2e-3
+
+
+@pytest.mark.parametrize("route", ["dequantize-first", "fused-8bit"])
+def test_c4_prefill_full_size(dev, route):
+    from locals_amd import sdpa
+
+    B, H, KVH, L, P = 1, 32, 8, 512, 16384
+    N = P + L
+    cap = (N + 255) // 256 * 256
+    print(f"C4 prefill full size, {route}", flush=True)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(41)
+    q, K, V = peaked_inputs_torch(gen, dev, B, H, KVH, L, cap, [0], [P], scale=SCALE, n_dom=3)
+    sinks = torch.randn((H,), generator=gen, device=dev).to(torch.float16) * 2
+    old = sdpa.DEQUANTIZE_FIRST
+    try:
+        sdpa.DEQUANTIZE_FIRST = route == "dequantize-first"
+        got = sdpa.scaled_dot_product_attention(q, tuple(t[:, :, :N] for t in K), tuple(t[:, :, :N] for t in V),
+                                                scale=SCALE, mask="causal", sinks=sinks)
+        torch.cuda.synchronize()
+    finally:
+        sdpa.DEQUANTIZE_FIRST = old
+    ref = cbind.sdpa_q8(q.cpu().numpy(), _host_triple(K), _host_triple(V), SCALE, "causal", sinks.cpu().numpy(),
+                        n=N, threads=16)
+    err = _err(got, ref)
+    print(f"  C4 prefill max |gpu - C| = {err:.3g}", flush=True)
+    assert err <= 2e-3
+
+
+def test_c4_decode_rows_full_size(dev):
+    """C4's decode part: 15 rows with contexts U[2k, 16k] (bench.py's draw), left-padded in one buffer."""
+    import bench
+    from locals_amd import qkv
+
+    cfg = bench.config("c4")
+    B, H, KVH, nb = cfg["B"], cfg["H"], cfg["KVH"], cfg["nb"]
+    n = int(nb.max())
+    cap = (n + 255) // 256 * 256
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(42)
+    start = n - nb
+    q, K, V = peaked_inputs_torch(gen, dev, B, H, KVH, 1, cap, start, np.full(B, n), scale=SCALE)
+    sinks = torch.randn((H,), generator=gen, device=dev) * 2
+    st = torch.tensor(start, dtype=torch.int32, device=dev)
+    got = qkv.attend(q, K, V, n, sinks, SCALE, st)
+    torch.cuda.synchronize()
+    ref = cbind.attend_q8(q.cpu().numpy(), _host_triple(K), _host_triple(V), n, sinks.cpu().numpy(), SCALE,
+                          start.astype(np.int32), threads=16)
+    err = _err(got, ref)
+    print(f"  C4 decode rows max |gpu - C| = {err:.3g}", flush=True)
+    assert err <= 2e-3
+
+
+def test_c5_tree_full_size(dev):
+    import bench
+    from locals_amd.sdpa import TreeMask, scaled_dot_product_attention
+
+    B, H, KVH, L, P = 8, 32, 8, 16, 8192
+    N = P + L
+    cap = (N + 255) // 256 * 256
+    print("C5 tree verification full size", flush=True)
+    g = np.random.default_rng(7)
+    trees = [bench.random_tree(g, L) for _ in range(B)]
+    local = np.zeros((B, L, L), bool)
+    for b, par in enumerate(trees):
+        for i in range(L):
+            j = i
+            while j >= 0:
+                local[b, i, j] = True
+                j = par[j]
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(51)
+    q, K, V = peaked_inputs_torch(gen, dev, B, H, KVH, L, cap, np.zeros(B, int), np.full(B, P), scale=SCALE)
+    mask = TreeMask.from_local(torch.from_numpy(local), device=dev)
+    got = scaled_dot_product_attention(q, tuple(t[:, :, :N] for t in K), tuple(t[:, :, :N] for t in V), scale=SCALE,
+                                       mask=mask)
+    torch.cuda.synchronize()
+    bits = (local.astype(np.uint64) << np.arange(L, dtype=np.uint64)).sum(-1).astype(np.uint64)
+    ref = cbind.sdpa_q8(q.cpu().numpy(), _host_triple(K), _host_triple(V), SCALE, "tree", None, n=N, tree=bits,
+                        threads=16)
+    err = _err(got, ref)
+    print(f"  C5 max |gpu - C| = {err:.3g}", flush=True)
+    assert err <= 2e-3

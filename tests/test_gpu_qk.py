@@ -144,6 +144,41 @@ def test_fused_append_equals_norm_rope_then_quantize(dev, dtype, mode):
             assert f.shape == p.shape and torch.equal(f, p), step
 
 
+@pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
+@pytest.mark.parametrize("mode", ["away", "even"])
+def test_fused_append_vs_oracle(dev, dtype, mode):
+    """qk_norm_rope_append against the oracle directly (locals/fuse.py:80-83 -> locals/qkv.py:309-326): q equals
+    oracle.attn.qk_norm_rope bit for bit, and the cache's new positions hold oracle.quant.quantize of the oracle's
+    normed/rotated k and of the raw v, bit for bit, in both tie modes.  A left-padded batch: a prompt chunk at
+    per-row offsets, then a decode step; positions outside [prev, prev + L) keep their earlier contents."""
+    from locals_amd import qk_kernel, qkv
+
+    H, KV, HD, B = 8, 2, 128, 3
+    a, qw, kw = _layer(H, KV, HD, dtype, dev, True, base=1000000.0, seed=3)
+    pads = [5, 0, 60]
+    cache = qkv.BatchQuantizedKVCache(pads, device=dev)
+    g = rng(9)
+    for L in (61, 1):
+        print(f"fused append vs oracle {dtype} {mode} L={L}", flush=True)
+        x = normal16(g, (B, L, (H + 2 * KV) * HD), 2.0, dtype)
+        offs = cache.offset.cpu().numpy().copy()  # positions of this step's first token, per row
+        prev = cache._idx
+        before = None if cache.keys is None else [t.clone() for t in cache.keys + cache.values]
+        q = qk_kernel.qk_norm_rope_append(to_torch(x, dev, dtype), a, cache, round_mode=mode)
+        torch.cuda.synchronize()
+        q0, k0, v0 = oa.qk_norm_rope(oq.to_f32(x, dtype), qw, kw, 1e-6, offs, H, KV, HD, True, 1000000.0, dtype)
+        assert np.array_equal(_f32(q), q0)
+        for buf, ref in ((cache.keys, k0), (cache.values, v0)):
+            rw, rs, rb = oq.quantize(oq.from_f32(ref, dtype), dtype, round_mode=mode)
+            w, s_, b_ = (t[:, :, prev:prev + L].cpu() for t in buf)
+            assert np.array_equal(w.numpy().view(np.uint32), rw)
+            assert np.array_equal(s_.view(torch.int16).numpy().view(np.uint16), np.asarray(rs).view(np.uint16))
+            assert np.array_equal(b_.view(torch.int16).numpy().view(np.uint16), np.asarray(rb).view(np.uint16))
+        if before is not None:
+            for t, o in zip(cache.keys + cache.values, before):
+                assert torch.equal(t[:, :, :prev], o[:, :, :prev])
+
+
 def test_fused_append_single_cache_and_attention(dev):
     """QuantizedKVCache8 (int offset) through the fused store, then attend_cache: equals the unfused
     qkv.attention(q, k, v, cache, ...) path on a twin cache."""

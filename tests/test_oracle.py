@@ -324,3 +324,43 @@ def test_qk_norm_rope_position_zero_is_the_norm_and_rope_is_relative():
         _, kp, _ = oa.qk_norm_rope(x, w, w, 1e-6, [p - 5], H, KV, HD, True)
         dots.append(float((qp[0, 0, 0].astype(np.float64) * kp[0, 0, 0]).sum()))
     assert abs(dots[0] - dots[1]) < 0.05 and abs(dots[0] - float((qn[0, 0, 0] * kn[0, 0, 0]).sum())) > 0.05
+
+
+@pytest.mark.parametrize("mask", [None, "causal", "tree", "dense", "window"])
+def test_c_sdpa_matches_float64_oracle(mask):
+    """The C masked SDPA (used for full-size GPU parity) against the float64 closed form on small cases: every mask
+    kind, sinks, left padding, G = 4, queries that cross its 16-query blocks; and the 8-bit form against sdpa_q8."""
+    g = np.random.default_rng(40)
+    B, H, KVH, L, N, D = 2, 8, 2, 21, 150, 128
+    cap = 160
+    q = g.standard_normal((B, H, L, D)).astype(np.float32)
+    k = g.standard_normal((B, KVH, cap, D)).astype(np.float32)
+    v = g.standard_normal((B, KVH, cap, D)).astype(np.float32)
+    sinks = (2 * g.standard_normal(H)).astype(np.float32)
+    start = np.array([0, 17], dtype=np.int32)
+    vis = np.broadcast_to(oa.causal_mask(L, N), (B, L, N)).copy()
+    kw = {}
+    if mask == "tree":
+        parents = [[-1] + [int(g.integers(max(0, i - 3), i)) for i in range(1, L)] for _ in range(B)]
+        local = np.stack([oa.ancestor_mask(p) for p in parents])
+        vis = np.stack([oa.tree_full_mask(m, N - L) for m in local])
+        bits = (local.astype(np.uint64) << np.arange(L, dtype=np.uint64)).sum(-1).astype(np.uint64)
+        kw["tree"] = bits
+    elif mask == "dense":
+        vis = g.random((B, L, N)) < 0.4
+        kw["dense"] = vis
+    elif mask == "window":
+        vis = np.broadcast_to(oa.window_mask(L, N, 37), (B, L, N)).copy()
+        kw["window"] = 37
+    elif mask is None:
+        vis = np.ones((B, L, N), bool)
+    vis = vis & (np.arange(N)[None, None, :] >= start[:, None, None])
+    got = cbind.sdpa(q, k, v, 0.0884, mask, sinks, start=start, n=N, **kw)
+    ref = oa.sdpa(q, k[:, :, :N], v[:, :, :N], 0.0884, vis[:, None], sinks, dtype="float64")
+    assert np.abs(got - ref).max() < 2e-6
+    if mask in ("causal", "tree"):
+        K, V = oq.quantize(k.astype(np.float16)), oq.quantize(v.astype(np.float16))
+        q16, s16 = q.astype(np.float16), sinks.astype(np.float16)
+        got8 = cbind.sdpa_q8(q16, K, V, 0.0884, mask, s16, n=N, start=start, **kw)
+        ref8 = oa.sdpa_q8(q16, K, V, 0.0884, vis[:, None], s16, n=N)
+        assert np.abs(got8 - ref8).max() < 2e-6
