@@ -70,6 +70,42 @@ class Events:
             self.hip.hipEventDestroy(e)
 
 
+def dist(us):
+    """median / p10 / p90 / mean of a sample of µs values"""
+    a = np.asarray(us, dtype=np.float64)
+    return {"median": round(float(np.median(a)), 2), "p10": round(float(np.percentile(a, 10)), 2),
+            "p90": round(float(np.percentile(a, 90)), 2), "mean": round(float(a.mean()), 2), "n": int(a.size)}
+
+
+def timed_loop(run, steps, warmup, stream, every):
+    """``warmup`` untimed calls, then ``steps`` timed ones.  Returns (µs a step over the region, pass-1 µs of the
+    sampled dispatches or None).  With ``every`` > 0 the pass-1 dispatch of every ``every``-th call records its own
+    start/stop events; that costs step time (so the region time of such a loop is not reported), and bracketing
+    back-to-back dispatches lengthens what their events measure (C2 pass 1: ~106 us every call against ~101 us every
+    4th call, the rocprofv3 figure), so samples are taken every 4th call.  With ``every`` = 0 the region has no other
+    events."""
+    import torch
+
+    for i in range(warmup):
+        run(i)
+    torch.cuda.synchronize()
+    ev = Events(2 * steps + 2)
+    hip = ev.hip
+    hip.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+    hip.hipEventRecord(ev.ev[-2], stream)
+    for i in range(steps):
+        if every and i % every == 0:
+            run(i, ev.ev[2 * i], ev.ev[2 * i + 1])
+        else:
+            run(i)
+    hip.hipEventRecord(ev.ev[-1], stream)
+    torch.cuda.synchronize()
+    step_us = ev.ms(2 * steps, 2 * steps + 1) * 1e3 / steps
+    p1 = [ev.ms(2 * i, 2 * i + 1) * 1e3 for i in range(0, steps, every)] if every else None
+    ev.close()
+    return step_us, p1
+
+
 def config(name: str, seed: int = 0):
     g = np.random.default_rng(seed)
     if name == "c1":
@@ -138,6 +174,13 @@ def random_tree(g, L=16, max_depth=8):
     return [-1 if parents[o] < 0 else new[parents[o]] for o in order]
 
 
+def _depth(parents, i):
+    d = 0
+    while parents[i] >= 0:
+        i, d = parents[i], d + 1
+    return d
+
+
 def bench_multi(cfg, args, dev):
     """C4 (decode rows + causal prefill chunk), C5 (tree verification) and W1 (sliding-window chunk over 16-bit K/V):
     pass-1 times from the dispatch events, FLOPs and bytes from the shapes."""
@@ -155,7 +198,9 @@ def bench_multi(cfg, args, dev):
     cap = (N + 255) // 256 * 256
     W = cfg.get("window", 0)
     sets = []
-    for s in range(args.sets):
+    kv_set = Bp * KVH * N * (512 if W else 272)
+    nsets = max(args.sets, -(-(1 << 30) // kv_set))  # >= 1 GiB of K/V in rotation, so the 256 MB MALL cannot hold it
+    for s in range(nsets):
         if W:  # 16-bit K/V, the rotating cache's dtype
             K = torch.randn((Bp, KVH, cap, 128), generator=gen, device=dev, dtype=torch.bfloat16)
             V = torch.randn((Bp, KVH, cap, 128), generator=gen, device=dev, dtype=torch.bfloat16)
@@ -199,7 +244,6 @@ def bench_multi(cfg, args, dev):
     route = "dequantize K/V, 16-bit pass 1" if nbytes > split else ("16-bit pass 1" if W else "fused 8-bit pass 1")
     ws = torch.empty(nbytes // 4 + 1, dtype=torch.float32, device=dev)
     out = torch.empty((Bp, H, L, 128), dtype=torch.bfloat16 if W else torch.float16, device=dev)
-    ev = Events(2 * args.steps + 2)
     P_ = _lib.ptr
 
     def run(i, e0=None, e1=None):
@@ -214,20 +258,20 @@ def bench_multi(cfg, args, dev):
                                  H, KVH, L, N, 128, cap, sdpa.BLOCK, P_(out), P_(ws), nbytes, stream, e0, e1)
         _lib.check(rc, "lcl_sdpa_ex")
 
-    for i in range(args.warmup):
-        run(i)
-    torch.cuda.synchronize()
-    for i in range(args.steps):
-        run(i, ev.ev[2 * i], ev.ev[2 * i + 1])
-    torch.cuda.synchronize()
-    t = np.array([ev.ms(2 * i, 2 * i + 1) for i in range(args.steps)])
-    ev.close()
-    us = float(t.mean() * 1e3)
+    # the whole call (dequantization, pass 1, join) unbracketed; then pass 1 of every 4th call by its own events
+    step_us, _ = timed_loop(run, args.steps, args.warmup, stream, 0)
+    _, p1 = timed_loop(run, 4 * args.steps, 2, stream, 4)
+    us = float(np.mean(p1))
     res = {"kernel": "sdpa_pass1", "route": route, "L": L, "N": N, "rows": Bp, "avg_us": round(us, 2),
-           "tflops": round(flops / (us * 1e-6) / 1e12, 1), "mfma_frac_of_2.5PF": round(flops / (us * 1e-6) / 2.5e15, 4),
-           "kv_GBs": round(kv_bytes / (us * 1e-6) / 1e9, 1), "flops": flops, "kv_bytes": kv_bytes}
+           "pass1_us": dist(p1), "tflops": round(flops / (us * 1e-6) / 1e12, 1),
+           "mfma_frac_of_2.5PF": round(flops / (us * 1e-6) / 2.5e15, 4),
+           "kv_GBs": round(kv_bytes / (us * 1e-6) / 1e9, 1), "hbm_frac": round(kv_bytes / (us * 1e-6) / 8e12, 4),
+           "us_per_call": round(step_us, 2),
+           "mfma_frac_call": round(flops / (step_us * 1e-6) / 2.5e15, 4),
+           "hbm_frac_call": round(kv_bytes / (step_us * 1e-6) / 8e12, 4),
+           "flops": flops, "kv_bytes": kv_bytes, "buffer_sets": nsets}
     if cfg["name"] == "c5":
-        res["trees"] = trees
+        res["tree_depths"] = [1 + max(_depth(t, i) for i in range(L)) for t in trees]
     if W:
         res["window"] = W
     return res
@@ -390,6 +434,64 @@ def build_sets(cfg, nsets, dev):
     return sets, start, n, cap
 
 
+def bench_decode_extra(cfg, args, dev):
+    """A decode config beside the headline (C3, C4's decode rows): the whole lcl_qkv_attend (pass 1 + join) over
+    >= 1 GiB of rotating buffer sets unbracketed, then pass 1 with its own dispatch events."""
+    import torch
+
+    from locals_amd import _lib, qkv
+
+    B, H, KVH = cfg["B"], cfg["H"], cfg["KVH"]
+    b_step, b_p1 = step_bytes(cfg)
+    nsets = max(2, -(-(1 << 30) // b_p1))
+    sets, start, n, cap = build_sets(cfg, nsets, dev)
+    lib = _lib.load()
+    nbytes = int(lib.lcl_decode_workspace_bytes(B, H, n, qkv.BLOCK))
+    ws = torch.empty(nbytes // 4 + 1, dtype=torch.float32, device=dev)
+    out = torch.empty((B, H, 1, 128), dtype=torch.float16, device=dev)
+    stream = _lib.stream_of(dev)
+
+    def run(i, e0=None, e1=None):
+        q, K, V = sets[i % len(sets)]
+        rc = lib.lcl_qkv_attend_ex(_lib.ptr(q), 0, _lib.ptr(K[0]), _lib.ptr(K[1]), _lib.ptr(K[2]), _lib.ptr(V[0]),
+                                   _lib.ptr(V[1]), _lib.ptr(V[2]), 0, _lib.ptr(start), None, float(1 / np.sqrt(128)),
+                                   B, H, KVH, 128, cap, n, qkv.BLOCK, _lib.ptr(out), _lib.ptr(ws), nbytes, stream, e0,
+                                   e1)
+        _lib.check(rc, "lcl_qkv_attend_ex")
+
+    steps, warmup = max(args.steps, 20), max(args.warmup, 3)
+    step_us, _ = timed_loop(run, steps, warmup, stream, 0)
+    _, p1 = timed_loop(run, 4 * steps, 2, stream, 4)
+    del sets
+    G = H // KVH
+    return {"workload": cfg["workload"], "B": B, "H": H, "KVH": KVH, "sum_n": int(cfg["nb"].sum()),
+            "us_per_step": round(step_us, 2), "hbm_frac_step": round(b_step / step_us / 1e3 / HBM_PEAK_GBS, 4),
+            "pass1": {"kernel": "qkv_pass1_q8_quad" if G <= 8 else "qkv_pass1_q8", "us": dist(p1),
+                      "hbm_frac": round(b_p1 / float(np.mean(p1)) / 1e3 / HBM_PEAK_GBS, 4)},
+            "bytes_per_step": b_step, "buffer_sets": nsets, "steps": steps}
+
+
+def extras(args, dev):
+    """The other BASELINE configurations measured in the same run: C3 (long-context split-K decode), C4 (the decode
+    rows and the 512-query prompt chunk of the hybrid batch) and C5 (tree verification), with kernel medians and
+    p10 / p90, HBM and MFMA fractions."""
+    import torch
+
+    a = argparse.Namespace(**vars(args))
+    a.steps, a.warmup = max(args.steps, 20), max(args.warmup, 3)
+    res = {"c3": bench_decode_extra(config("c3"), a, dev)}
+    torch.cuda.empty_cache()
+    c4d = bench_decode_extra(config("c4d"), a, dev)
+    torch.cuda.empty_cache()
+    c4p = bench_multi(config("c4"), a, dev)
+    torch.cuda.empty_cache()
+    res["c4"] = {"decode_rows": c4d, "prefill": c4p,
+                 "us_per_step_decode_then_prefill": round(c4d["us_per_step"] + c4p["us_per_call"], 2)}
+    res["c5"] = bench_multi(config("c5"), a, dev)
+    torch.cuda.empty_cache()
+    return res
+
+
 def step_bytes(cfg):
     B, H, KVH = cfg["B"], cfg["H"], cfg["KVH"]
     kv = int(cfg["nb"].sum()) * KVH * 272
@@ -444,6 +546,7 @@ def main():
     ap.add_argument("--block", type=int, default=None, help="keys a pass-1 workgroup reads (qkv.BLOCK)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-extras", action="store_true", help="skip C3 / C4 / C5 beside the headline")
     ap.add_argument("--p1-every", type=int, default=4, metavar="K",
                     help="bracket every K-th step's pass-1 dispatch with HIP events (the roofline sample)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
@@ -526,6 +629,8 @@ def main():
     region_ms = ev.ms(2 * K_, 2 * K_ + 1)
     p1 = np.array([ev.ms(2 * i, 2 * i + 1) for i in range(0, K_, every)])
     ev.close()
+    # after the timed region, for pass 1's distribution: 80 more steps, every 4th dispatch bracketed
+    _, p1_more = timed_loop(step, 80, 2, stream, 4)
     # secondary rooflines, outside the timed region: what a plain 1 GiB device copy and a plain streaming read of
     # 1 GiB move per second on this part
     copy_gbs = 2 * (1 << 30) / copy_ms(1 << 30, 20, dev) / 1e6
@@ -560,8 +665,11 @@ def main():
                    "wall_s_timed": round(wall, 4)},
         "roofline": {"bound": "hbm", "kernel": kernel, "achieved": round(achieved, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "avg_us": round(p1_us, 2), "p10_us": round(float(np.percentile(p1, 10)) * 1e3, 2),
-                     "p90_us": round(float(np.percentile(p1, 90)) * 1e3, 2), "bytes_per_launch": b_p1,
+                     "avg_us": round(p1_us, 2), "median_us": round(float(np.median(p1)) * 1e3, 2),
+                     "p10_us": round(float(np.percentile(p1, 10)) * 1e3, 2),
+                     "p90_us": round(float(np.percentile(p1, 90)) * 1e3, 2), "samples": int(p1.size),
+                     "sampled_every": every, "after_region_us": dist(p1_more),
+                     "bytes_per_launch": b_p1,
                      "traffic": _traffic(cfg["name"], kernel),
                      "measured_copy_GBs": round(copy_gbs, 1), "frac_of_measured_copy": round(achieved / copy_gbs, 4),
                      "measured_read_GBs": round(read_gbs, 1), "measured_read_setting": read_how,
@@ -578,6 +686,10 @@ def main():
                                 "sample": f"{reps} whole steps of buffer set 0 (the same inputs as the GPU), "
                                           f"C restatement of qkv.py's two passes (oracle/c/oracle.c), OpenMP",
                                 "max_abs_diff_vs_gpu": err}
+    if cfg["name"] == "c2" and not args.no_extras:
+        del sets, outs, ws
+        torch.cuda.empty_cache()
+        line["extras"] = extras(args, dev)
     print(json.dumps(line), flush=True)
 
 
