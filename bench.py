@@ -181,7 +181,7 @@ def _depth(parents, i):
     return d
 
 
-def bench_multi(cfg, args, dev):
+def bench_multi(cfg, args, dev, return_runner=False):
     """C4 (decode rows + causal prefill chunk), C5 (tree verification) and W1 (sliding-window chunk over 16-bit K/V):
     pass-1 times from the dispatch events, FLOPs and bytes from the shapes."""
     import torch
@@ -246,17 +246,21 @@ def bench_multi(cfg, args, dev):
     out = torch.empty((Bp, H, L, 128), dtype=torch.bfloat16 if W else torch.float16, device=dev)
     P_ = _lib.ptr
 
-    def run(i, e0=None, e1=None):
+    def run(i, e0=None, e1=None, st=None):
         q, K, V = sets[i % len(sets)]
+        st = stream if st is None else st
         if W:
             rc = lib.lcl_sdpa_ex(P_(q), 1, 1, None, None, None, None, None, None, P_(K), P_(V), 1, None, mk, W, None,
                                  0, None, 0, 0, 0, 0, None, float(1 / np.sqrt(128)), Bp, H, KVH, L, N, 128, cap,
-                                 sdpa.BLOCK, P_(out), P_(ws), nbytes, stream, e0, e1)
+                                 sdpa.BLOCK, P_(out), P_(ws), nbytes, st, e0, e1)
         else:
             rc = lib.lcl_sdpa_ex(P_(q), 0, 0, P_(K[0]), P_(K[1]), P_(K[2]), P_(V[0]), P_(V[1]), P_(V[2]), None, None,
                                  0, None, mk, 0, P_(tree), tree_bs, None, 0, 0, 0, 0, None, float(1 / np.sqrt(128)), Bp,
-                                 H, KVH, L, N, 128, cap, sdpa.BLOCK, P_(out), P_(ws), nbytes, stream, e0, e1)
+                                 H, KVH, L, N, 128, cap, sdpa.BLOCK, P_(out), P_(ws), nbytes, st, e0, e1)
         _lib.check(rc, "lcl_sdpa_ex")
+
+    if return_runner:
+        return run
 
     # the whole call (dequantization, pass 1, join) unbracketed; then pass 1 of every 4th call by its own events
     step_us, _ = timed_loop(run, args.steps, args.warmup, stream, 0)
@@ -434,7 +438,7 @@ def build_sets(cfg, nsets, dev):
     return sets, start, n, cap
 
 
-def bench_decode_extra(cfg, args, dev):
+def bench_decode_extra(cfg, args, dev, return_runner=False):
     """A decode config beside the headline (C3, C4's decode rows): the whole lcl_qkv_attend (pass 1 + join) over
     >= 1 GiB of rotating buffer sets unbracketed, then pass 1 with its own dispatch events."""
     import torch
@@ -451,13 +455,16 @@ def bench_decode_extra(cfg, args, dev):
     out = torch.empty((B, H, 1, 128), dtype=torch.float16, device=dev)
     stream = _lib.stream_of(dev)
 
-    def run(i, e0=None, e1=None):
+    def run(i, e0=None, e1=None, st=None):
         q, K, V = sets[i % len(sets)]
         rc = lib.lcl_qkv_attend_ex(_lib.ptr(q), 0, _lib.ptr(K[0]), _lib.ptr(K[1]), _lib.ptr(K[2]), _lib.ptr(V[0]),
                                    _lib.ptr(V[1]), _lib.ptr(V[2]), 0, _lib.ptr(start), None, float(1 / np.sqrt(128)),
-                                   B, H, KVH, 128, cap, n, qkv.BLOCK, _lib.ptr(out), _lib.ptr(ws), nbytes, stream, e0,
-                                   e1)
+                                   B, H, KVH, 128, cap, n, qkv.BLOCK, _lib.ptr(out), _lib.ptr(ws), nbytes,
+                                   stream if st is None else st, e0, e1)
         _lib.check(rc, "lcl_qkv_attend_ex")
+
+    if return_runner:
+        return run
 
     steps, warmup = max(args.steps, 20), max(args.warmup, 3)
     step_us, _ = timed_loop(run, steps, warmup, stream, 0)
@@ -469,6 +476,47 @@ def bench_decode_extra(cfg, args, dev):
             "pass1": {"kernel": "qkv_pass1_q8_quad" if G <= 8 else "qkv_pass1_q8", "us": dist(p1),
                       "hbm_frac": round(b_p1 / float(np.mean(p1)) / 1e3 / HBM_PEAK_GBS, 4)},
             "bytes_per_step": b_step, "buffer_sets": nsets, "steps": steps}
+
+
+def c4_overlap(args, dev):
+    """C4's two attention calls (the 15 decode rows, the 512-query prompt chunk) in sequence on one stream, and
+    concurrently on two streams of the default priority forked from and joined to it by events (what a
+    co-scheduled mixed.forward layer would launch, locals/mixed.py:108-110).  µs a step of both, over the region."""
+    import torch
+
+    from locals_amd import _lib
+
+    dec = bench_decode_extra(config("c4d"), args, dev, return_runner=True)
+    pre = bench_multi(config("c4"), args, dev, return_runner=True)
+    s0 = torch.cuda.current_stream(dev)
+    s1, s2 = torch.cuda.Stream(dev), torch.cuda.Stream(dev)
+    h1, h2 = ctypes.c_void_p(s1.cuda_stream), ctypes.c_void_p(s2.cuda_stream)
+
+    def seq(i, e0=None, e1=None):
+        dec(i)
+        pre(i)
+
+    def conc(i, e0=None, e1=None):
+        fork = torch.cuda.Event()
+        fork.record(s0)
+        s1.wait_event(fork)
+        s2.wait_event(fork)
+        dec(i, st=h1)
+        pre(i, st=h2)
+        d1, d2 = torch.cuda.Event(), torch.cuda.Event()
+        d1.record(s1)
+        d2.record(s2)
+        s0.wait_event(d1)
+        s0.wait_event(d2)
+
+    stream = _lib.stream_of(dev)
+    steps, warmup = max(args.steps, 20), max(args.warmup, 3)
+    out = {}
+    for rep_ in range(2):  # interleaved, twice
+        out.setdefault("sequential_us", []).append(round(timed_loop(seq, steps, warmup, stream, 0)[0], 2))
+        out.setdefault("concurrent_us", []).append(round(timed_loop(conc, steps, warmup, stream, 0)[0], 2))
+    torch.cuda.synchronize()
+    return out
 
 
 def extras(args, dev):
@@ -486,7 +534,9 @@ def extras(args, dev):
     c4p = bench_multi(config("c4"), a, dev)
     torch.cuda.empty_cache()
     res["c4"] = {"decode_rows": c4d, "prefill": c4p,
-                 "us_per_step_decode_then_prefill": round(c4d["us_per_step"] + c4p["us_per_call"], 2)}
+                 "us_per_step_decode_then_prefill": round(c4d["us_per_step"] + c4p["us_per_call"], 2),
+                 "two_streams": c4_overlap(a, dev)}
+    torch.cuda.empty_cache()
     res["c5"] = bench_multi(config("c5"), a, dev)
     torch.cuda.empty_cache()
     return res
