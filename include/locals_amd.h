@@ -106,6 +106,18 @@ int lcl_quantize_append(const void* k, const void* v, int dt, uint32_t* kw, void
                         void* vs, void* vb, int B, int KVH, int L, int D, int cap, int prev, int round_mode,
                         void* stream);
 
+/* The buffer moves of BatchQuantizedKVCache's row bookkeeping -- merge (locals/qkv.py:417-431), extend
+ * (:382-406), filter (:370-380), extract (:408-415) and finalize's roll (:340-346, mlx-lm dynamic_roll) -- as one
+ * gather into a new triple: words dw (rows, KVH, cap, D/4) uint32, scales ds and biases db (rows, KVH, cap, D/64)
+ * 16-bit.  Destination row r reads the source triple (src_w[r], src_s[r], src_b[r]) -- pointers to that row's
+ * (kv head 0, position 0), src_cap[r] positions a kv head -- at position t - shift[r]: wrap[r] == 0 copies it when
+ * it lies in [0, len[r]) and writes 0 elsewhere; wrap[r] == 1 takes it modulo len[r] (the roll).  The row
+ * arrays are host memory (len rows each); a row with len 0 is all zeros and its pointers may be NULL.  The copy
+ * is exact.  D a multiple of 64. */
+int lcl_kv_gather(uint32_t* dw, void* ds, void* db, int rows, int KVH, int cap, int D, const uint32_t* const* src_w,
+                  const void* const* src_s, const void* const* src_b, const long long* src_cap, const int* shift,
+                  const int* len, const int* wrap, void* stream);
+
 /* qkv.dequantized (locals/qkv.py:252-253, mx.dequantize): rows of D values
  * scale * code + bias from (rows, D/4) words and (rows, D/64) scales/biases of
  * dtype sdt, written as dtype odt (f16, bf16 or f32). */

@@ -36,6 +36,7 @@ SIGNATURES = {
     "lcl_ragged_attention_ex": (I, [P, I, P, P, I, P, P, F, P, I, I, I, I, I, I, I, P, P, Z, P, P, P]),
     "lcl_quantize_append": (I, [P, P, I, P, P, P, P, P, P, I, I, I, I, I, I, I, P]),
     "lcl_dequantize": (I, [P, P, P, I, ctypes.c_longlong, I, P, I, P]),
+    "lcl_kv_gather": (I, [P, P, P, I, I, I, I, P, P, P, P, P, P, P, P]),
     "lcl_sdpa_workspace_bytes": (Z, [I, I, I, I, I]),
     "lcl_sdpa_workspace_bytes_kv": (Z, [I, I, I, I, I, I, I, I, I]),
     "lcl_sdpa": (I, [P, I, I, P, P, P, P, P, P, P, P, I, P, I, I, P, LL, P, LL, LL, LL, LL, P, F, I, I, I, I, I, I, I, I,

@@ -14,6 +14,7 @@ Nothing here synchronises with the GPU except where the reference itself reads v
 
 from __future__ import annotations
 
+import ctypes
 import os
 from typing import List, Optional
 
@@ -244,14 +245,39 @@ def create_causal_mask(N: int, offset: int = 0, window_size: Optional[int] = Non
     return mask
 
 
-def dynamic_roll(a: torch.Tensor, shifts: torch.Tensor, axis: int = 2) -> torch.Tensor:
-    """mlx-lm's ``dynamic_roll`` along ``axis`` with one shift a row (row = dim 0), used by ``finalize``."""
-    n = a.shape[axis]
-    idx = (torch.arange(n, device=a.device)[None, :] - shifts.reshape(-1, 1).to(a.device)) % n  # (B, n)
-    shape = [a.shape[0]] + [1] * (a.dim() - 1)
-    shape[axis] = n
-    idx = idx.reshape(shape).expand_as(a)
-    return torch.gather(a, axis, idx)
+def move_rows(rows, cap: int, like):
+    """New (keys, values) triples of ``len(rows)`` rows and ``cap`` positions, built on the GPU by ``lcl_kv_gather``
+    (one launch a triple).  ``rows[r] = (keys, values, row, shift, n, wrap)``: destination row r takes row ``row``
+    of the source triples at position t - shift -- copied where it lies in [0, n), 0 elsewhere; with ``wrap``
+    modulo n (a roll).  A source of None (or n == 0) gives a zero row.  ``like`` is a (keys, values) pair whose
+    kv heads, head dims and dtypes the result takes."""
+    lk, lv = like
+    KVH, dt, dev = lk[0].shape[1], lk[1].dtype, lk[0].device
+    out = []
+    for which, ref in ((0, lk), (1, lv)):
+        D = _head_dim(ref)
+        dst = _zeros_like_shape(len(rows), KVH, cap, D, dt, dev, empty=True)
+        n_ = len(rows)
+        PP = ctypes.c_void_p * n_
+        sw, ss, sb = PP(), PP(), PP()
+        scap = (ctypes.c_longlong * n_)()
+        sh, ln, wr = (ctypes.c_int * n_)(), (ctypes.c_int * n_)(), (ctypes.c_int * n_)()
+        for r, (keys, values, row, shift, n, wrap) in enumerate(rows):
+            src = keys if which == 0 else values
+            n = int(n) if src is not None else 0
+            if n:
+                if src[0].device != dev or not all(a.is_contiguous() for a in src):
+                    raise ValueError("row moves need contiguous buffers on the same GPU")
+                sw[r], ss[r], sb[r] = (ctypes.c_void_p(a[row].data_ptr()) for a in src)
+                scap[r] = src[0].shape[2]
+            sh[r], ln[r], wr[r] = int(shift), n, int(bool(wrap))
+        if n_ and cap:
+            _lib.require_gpu(*dst)
+            rc = _lib.load().lcl_kv_gather(_lib.ptr(dst[0]), _lib.ptr(dst[1]), _lib.ptr(dst[2]), n_, KVH, cap, D, sw,
+                                           ss, sb, scap, sh, ln, wr, _lib.stream_of(dev))
+            _lib.check(rc, "lcl_kv_gather")
+        out.append(dst)
+    return out[0], out[1]
 
 
 def _grow(cache, B: int, H: int, prev: int, S: int, D: int, dtype, device, keep_aligned: bool = False) -> None:
@@ -314,6 +340,23 @@ class QuantizedKVCache8:
     def state(self, v):
         self.keys, self.values = v
         self.offset = self.keys[0].shape[2]
+
+    @property
+    def meta_state(self):
+        """(step, offset, group_size, bits) as strings, as mlx-lm's QuantizedKVCache records them in a snapshot."""
+        return tuple(map(str, (self.step, self.offset, self.group_size, self.bits)))
+
+    @meta_state.setter
+    def meta_state(self, v):
+        self.step, self.offset, self.group_size, self.bits = map(int, v)
+
+    @classmethod
+    def from_state(cls, state, meta_state):
+        c = cls.__new__(cls)
+        c.keys = c.values = None
+        c.state = state
+        c.meta_state = meta_state
+        return c
 
     def is_trimmable(self):
         return True
@@ -398,15 +441,20 @@ class BatchQuantizedKVCache:
             self.left_padding = self.left_padding + lp
             self.offset = self.offset - lp
         if right_padding is not None and max(right_padding) > 0:
-            self._right_padding = torch.as_tensor(right_padding, dtype=torch.int32, device=self._dev())
+            self._right_padding = [int(x) for x in right_padding]  # host values: the roll's shifts
 
     def finalize(self):
+        """Rows prepared with right padding are rolled right by it (mlx-lm's dynamic_roll along the positions), so
+        their padding moves to the left (locals/qkv.py:340-346)."""
         if self._right_padding is not None:
             p = self._right_padding
-            self.keys = tuple(dynamic_roll(a, p) for a in self.keys)
-            self.values = tuple(dynamic_roll(a, p) for a in self.values)
-            self.offset = self.offset - p
-            self.left_padding = self.left_padding + p
+            if self.keys is not None:
+                n = self.keys[0].shape[2]
+                self.keys, self.values = move_rows([(self.keys, self.values, b, p[b], n, True) for b in range(len(p))],
+                                                   n, (self.keys, self.values))
+            pt = torch.as_tensor(p, dtype=torch.int32, device=self._dev())
+            self.offset = self.offset - pt
+            self.left_padding = self.left_padding + pt
             self._right_padding = None
 
     @property
@@ -430,17 +478,19 @@ class BatchQuantizedKVCache:
         return create_causal_mask(N, offset=self._idx, left_padding=self.left_padding, device=self._dev(), **kwargs)
 
     def filter(self, batch_indices):
-        idx = torch.as_tensor(batch_indices, device=self._dev(), dtype=torch.long)
-        if self.keys is not None:
-            self.keys = tuple(a[idx] for a in self.keys)
-            self.values = tuple(a[idx] for a in self.values)
+        """Keep the rows ``batch_indices`` (in that order) and drop the left padding they all share
+        (locals/qkv.py:370-380): one gather of the kept rows shifted left by that padding."""
+        keep = [int(i) for i in (batch_indices.tolist() if isinstance(batch_indices, torch.Tensor) else batch_indices)]
+        idx = torch.as_tensor(keep, device=self._dev(), dtype=torch.long)
         self.offset = self.offset[idx]
         self.left_padding = self.left_padding[idx]
         drop = int(self.left_padding.min().item()) if self.left_padding.numel() else 0
+        drop = max(drop, 0)
+        if self.keys is not None:
+            n = self.keys[0].shape[2]
+            self.keys, self.values = move_rows([(self.keys, self.values, i, -drop, n, False) for i in keep], n - drop,
+                                               (self.keys, self.values))
         if drop > 0:
-            if self.keys is not None:
-                self.keys = tuple(a[..., drop:, :].contiguous() for a in self.keys)
-                self.values = tuple(a[..., drop:, :].contiguous() for a in self.values)
             self._idx -= drop
             self.left_padding = self.left_padding - drop
 
@@ -450,36 +500,30 @@ class BatchQuantizedKVCache:
             self.offset = torch.cat([self.offset, other.offset.to(self._dev())])
             return
         ref = self if self.keys is not None else other
-        H, D, M, dtype = ref.keys[0].shape[1], _head_dim(ref.keys), _head_dim(ref.values), ref.keys[1].dtype
         dev = ref.keys[0].device
         max_idx = max(self._idx, other._idx)
         size = max(c.keys[0].shape[2] for c in (self, other) if c.keys is not None)
-
-        def pad(c):
-            k = c.keys if c.keys is not None else _zeros(c.offset.shape[0], H, 0, D, dtype, dev)
-            v = c.values if c.values is not None else _zeros(c.offset.shape[0], H, 0, M, dtype, dev)
+        # each side's rows move right by max_idx - _idx; what passes `size` is cut, the rest is zero-filled
+        # (locals/qkv.py:388-401)
+        rows = []
+        for c in (self, other):
             left = max_idx - c._idx
-            right = size - k[0].shape[2] - left
-            if right < 0:
-                k, v = _slice(k, None, right), _slice(v, None, right)
-                right = 0
-            if left or right:
-                k = tuple(torch.nn.functional.pad(a, (0, 0, left, right)) for a in k)
-                v = tuple(torch.nn.functional.pad(a, (0, 0, left, right)) for a in v)
-            return k, v, c.offset.to(dev), c.left_padding.to(dev) + left
-
-        (k1, v1, o1, p1), (k2, v2, o2, p2) = pad(self), pad(other)
-        self.keys = tuple(torch.cat([a, b]) for a, b in zip(k1, k2))
-        self.values = tuple(torch.cat([a, b]) for a, b in zip(v1, v2))
-        self.offset, self.left_padding = torch.cat([o1, o2]), torch.cat([p1, p2])
+            n = min(c.keys[0].shape[2], size - left) if c.keys is not None else 0
+            rows += [(c.keys, c.values, b, left, n, False) for b in range(c.offset.shape[0])]
+        self.keys, self.values = move_rows(rows, size, (ref.keys, ref.values))
+        self.offset = torch.cat([self.offset.to(dev), other.offset.to(dev)])
+        self.left_padding = torch.cat([self.left_padding.to(dev) + (max_idx - self._idx),
+                                       other.left_padding.to(dev) + (max_idx - other._idx)])
         self._idx = max_idx
 
     def extract(self, idx):
+        """Row ``idx`` as a one-request cache holding exactly its positions [left_padding, _idx)
+        (locals/qkv.py:408-415)."""
         c = QuantizedKVCache8()
         p = int(self.left_padding[idx].item())
-        c.keys = tuple(a[idx:idx + 1, :, p:self._idx].contiguous() for a in self.keys)
-        c.values = tuple(a[idx:idx + 1, :, p:self._idx].contiguous() for a in self.values)
-        c.offset = c.keys[0].shape[2]
+        c.keys, c.values = move_rows([(self.keys, self.values, int(idx), -p, self._idx, False)], self._idx - p,
+                                     (self.keys, self.values))
+        c.offset = self._idx - p
         return c
 
     @classmethod
@@ -491,15 +535,10 @@ class BatchQuantizedKVCache:
         out = cls([L - n for n in lengths], device=dev)
         if L == 0:
             return out
-        H, D, M, dtype = ref.keys[0].shape[1], _head_dim(ref.keys), _head_dim(ref.values), ref.keys[1].dtype
-        keys, values = _zeros(len(caches), H, L, D, dtype, dev), _zeros(len(caches), H, L, M, dtype, dev)
-        for i, (n, c) in enumerate(zip(lengths, caches)):
-            if n:
-                for a, x in zip(keys, c.keys):
-                    a[i:i + 1, :, L - n:] = x[..., :n, :]
-                for a, x in zip(values, c.values):
-                    a[i:i + 1, :, L - n:] = x[..., :n, :]
-        out.keys, out.values, out._idx = keys, values, L
+        # request i's first n_i positions, right-aligned in L (locals/qkv.py:419-430)
+        out.keys, out.values = move_rows([(c.keys, c.values, 0, L - n, n, False) for n, c in zip(lengths, caches)],
+                                         L, (ref.keys, ref.values))
+        out._idx = L
         out.offset = out.offset + L
         return out
 
@@ -535,3 +574,87 @@ def opt_in(model) -> Optional[bool]:
 
     model.make_cache = make_cache
     return True
+
+
+# ---- prompt-cache snapshots (the reference's DiskPromptCache, locals/hybrid_batch.py:332-455, writes them with
+# mlx-lm's save_prompt_cache / load_prompt_cache): one safetensors file, each layer cache's ``state`` arrays under
+# "<layer>.<i>.<j>" and, in the metadata, its ``meta_state`` under "0.<layer>.<k>", the caller's metadata under
+# "1.<key>" and its class name under "2.<layer>".  The 8-bit words are stored as uint32, as MLX holds them.
+
+_SNAPSHOT_CLASSES = {"QuantizedKVCache8": QuantizedKVCache8}
+
+
+def _flatten(tree, prefix=""):
+    if isinstance(tree, (list, tuple)):
+        out = []
+        for i, t in enumerate(tree):
+            out += _flatten(t, f"{prefix}.{i}" if prefix else str(i))
+        return out
+    if isinstance(tree, dict):
+        out = []
+        for k, t in tree.items():
+            out += _flatten(t, f"{prefix}.{k}" if prefix else str(k))
+        return out
+    return [(prefix, tree)]
+
+
+def _unflatten(items):
+    """The nested lists of _flatten's numeric paths (and dicts of the others)."""
+    root: dict = {}
+    for key, val in items:
+        node = root
+        parts = key.split(".")
+        for part in parts[:-1]:
+            node = node.setdefault(part, {})
+        node[parts[-1]] = val
+
+    def build(node):
+        if not isinstance(node, dict):
+            return node
+        if node and all(k.isdigit() for k in node):  # a list; an empty one leaves no key behind
+            return [build(node.get(str(i), {})) for i in range(max(int(k) for k in node) + 1)]
+        return {k: build(v) for k, v in node.items()}
+
+    return build(root)
+
+
+def save_prompt_cache(path: str, caches, metadata: Optional[dict] = None) -> None:
+    """Write the layer caches ``caches`` (QuantizedKVCache8) to ``path`` in mlx-lm's snapshot layout."""
+    from safetensors.torch import save_file
+
+    arrays = {}
+    for key, t in _flatten([c.state for c in caches]):
+        t = t.detach().contiguous().cpu()
+        if t.dtype == torch.int32:  # 8-bit words
+            t = t.view(torch.uint32)
+        arrays[key] = t
+    meta = dict(_flatten([[c.meta_state for c in caches], metadata or {}, [type(c).__name__ for c in caches]]))
+    save_file(arrays, path, metadata={k: str(v) for k, v in meta.items()})
+
+
+def load_prompt_cache(path: str, device=None, return_metadata: bool = False):
+    """The layer caches of a snapshot written by ``save_prompt_cache`` (or mlx-lm's, for 8-bit layers), on
+    ``device`` (default cuda:0)."""
+    from safetensors import safe_open
+
+    dev = torch.device(device) if device is not None else torch.device("cuda", 0)
+    with safe_open(path, "pt") as f:
+        meta = f.metadata() or {}
+        arrays = []
+        for k in f.keys():
+            t = f.get_tensor(k)
+            if t.dtype == getattr(torch, "uint32", None):
+                t = t.view(torch.int32)
+            arrays.append((k, t.to(dev)))
+    state = _unflatten(arrays)
+    info, user_meta, classes = (_unflatten(list(meta.items())) + [None, None, None])[:3]
+    caches = []
+    for i, name in enumerate(classes):
+        cls = _SNAPSHOT_CLASSES.get(name)
+        if cls is None:
+            raise ValueError(f"snapshot layer {i}: cache class {name!r} is not one of {sorted(_SNAPSHOT_CLASSES)}")
+        st = state[i]
+        caches.append(cls.from_state((tuple(st[0]), tuple(st[1])), info[i]))
+    if return_metadata:
+        return caches, (user_meta if isinstance(user_meta, dict) else {})
+    return caches

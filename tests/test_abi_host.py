@@ -103,16 +103,13 @@ def test_python_wrappers_refuse_cpu_tensors():
         qkv.attend(q, K, K, 10, None, 0.1, None)
 
 
-def test_create_causal_mask_and_dynamic_roll():
+def test_create_causal_mask():
     from locals_amd import qkv
 
     m = qkv.create_causal_mask(3, offset=4)
     assert m.shape == (3, 7) and m[0].tolist() == [True] * 5 + [False] * 2 and m[2].all()
     mp = qkv.create_causal_mask(2, offset=3, left_padding=torch.tensor([0, 2]))
     assert mp.shape == (2, 1, 2, 5) and not mp[1, 0, :, :2].any() and mp[0, 0, 1].all()
-    a = torch.arange(10).reshape(2, 1, 5, 1)
-    r = qkv.dynamic_roll(a, torch.tensor([1, 3]))
-    assert r[0, 0, :, 0].tolist() == [4, 0, 1, 2, 3] and r[1, 0, :, 0].tolist() == [7, 8, 9, 5, 6]
 
 
 def _filled(B, H, n, seed):
@@ -126,37 +123,6 @@ def _filled(B, H, n, seed):
     return t
 
 
-def test_batch_cache_merge_extend_filter_extract_on_host():
-    """Row bookkeeping of BatchQuantizedKVCache on CPU buffers: merge left-pads, extend aligns, filter drops the
-    common padding, extract returns a row's own keys."""
-    from locals_amd import qkv
-
-    c1, c2 = qkv.QuantizedKVCache8(), qkv.QuantizedKVCache8()
-    c1.keys, c1.values, c1.offset = _filled(1, 2, 256, 1), _filled(1, 2, 256, 2), 20
-    c2.keys, c2.values, c2.offset = _filled(1, 2, 256, 3), _filled(1, 2, 256, 4), 11
-    b = qkv.QuantizedKVCache8.merge([c1, c2])
-    assert b._idx == 20 and b.left_padding.tolist() == [0, 9] and b.offset.tolist() == [20, 11]
-    for a, x in zip(b.keys, c2.keys):
-        assert torch.equal(a[1, :, 9:20], x[0, :, :11])
-    # extract row 1 = c2's keys exactly
-    e = b.extract(1)
-    assert e.offset == 11 and all(torch.equal(a[0], x[0, :, :11]) for a, x in zip(e.keys, c2.keys))
-    # extend with a longer batch: the shorter side is padded on the left
-    c3 = qkv.QuantizedKVCache8()
-    c3.keys, c3.values, c3.offset = _filled(1, 2, 256, 5), _filled(1, 2, 256, 6), 30
-    b3 = qkv.QuantizedKVCache8.merge([c3])
-    b.extend(b3)
-    assert b._idx == 30 and b.left_padding.tolist() == [10, 19, 0] and b.offset.tolist() == [20, 11, 30]
-    for a, x in zip(b.keys, c1.keys):
-        assert torch.equal(a[0, :, 10:30], x[0, :, :20])
-    # filter rows [0, 1]: their common padding 10 is dropped
-    b.filter([0, 1])
-    assert b._idx == 20 and b.left_padding.tolist() == [0, 9]
-    for a, x in zip(b.keys, c1.keys):
-        assert torch.equal(a[0, :, :20], x[0, :, :20])
-    assert b.nbytes == sum(a.numel() * a.element_size() for a in b.keys + b.values)
-
-
 def test_batch_cache_growth_follows_the_reference_rule():
     """BatchQuantizedKVCache grows to prev + ceil(S / 256) * 256 positions, keeping exactly the first prev
     (locals/qkv.py:311-319: concatenate(a[..., :prev, :], zeros(ceil(S / step) * step))).  Capacities below are
@@ -167,12 +133,10 @@ def test_batch_cache_growth_follows_the_reference_rule():
         c._reserve(c.left_padding.numel(), 2, S, 128, torch.float16, torch.device("cpu"))
         return c.keys[0].shape[2]
 
-    # merge (700 and 300 keys: buffers of exactly 700) then decode steps
-    c1, c2 = qkv.QuantizedKVCache8(), qkv.QuantizedKVCache8()
-    c1.keys, c1.values, c1.offset = _filled(1, 2, 768, 1), _filled(1, 2, 768, 2), 700
-    c2.keys, c2.values, c2.offset = _filled(1, 2, 512, 3), _filled(1, 2, 512, 4), 300
-    b = qkv.QuantizedKVCache8.merge([c1, c2])
-    assert b.keys[0].shape[2] == 700
+    # as merge leaves two requests of 700 and 300 keys (buffers of exactly 700 positions), then decode steps
+    b = qkv.BatchQuantizedKVCache([0, 400])
+    b.keys, b.values, b._idx = _filled(2, 2, 700, 1), _filled(2, 2, 700, 2), 700
+    b.offset = torch.tensor([700, 300], dtype=torch.int32)
     assert step(b, 1) == 956  # 700 + 256
     assert step(b, 255) == 956  # 956 positions used, no growth
     assert step(b, 1) == 1212  # 956 + 256
@@ -193,9 +157,6 @@ def test_batch_cache_growth_follows_the_reference_rule():
     assert step(e2, 10) == 556
     assert all(torch.equal(a[..., :300, :], o) for a, o in zip(e2.keys, old))
     assert not any(a[..., 300:, :].any() for a in e2.keys)
-    # extend takes the larger capacity of the two sides
-    b.extend(e)
-    assert b.keys[0].shape[2] == 1213 and b._idx == 1001
 
 
 def test_single_cache_growth_follows_mlx_lm():
@@ -236,3 +197,31 @@ def test_prompt_branch_hands_sinks_over_in_the_query_dtype(monkeypatch):
     assert seen["sinks"].dtype == torch.bfloat16 and torch.equal(seen["sinks"], s32.to(torch.bfloat16))
     qkv.attend_cache(q, c, 0.1, "causal", None)
     assert seen["sinks"] is None
+
+
+def test_prompt_cache_snapshot_layout_on_host(tmp_path):
+    """save_prompt_cache writes mlx-lm's layout (state arrays under "<layer>.<i>.<j>", meta_state, metadata and
+    class names in the safetensors metadata; 8-bit words as uint32) and load_prompt_cache reads it back exactly."""
+    from safetensors import safe_open
+
+    from locals_amd import qkv
+
+    caches = []
+    for i, n in enumerate((300, 17)):
+        c = qkv.QuantizedKVCache8()
+        c.keys, c.values, c.offset = _filled(1, 2, 512, 10 + i), _filled(1, 2, 512, 20 + i), n
+        caches.append(c)
+    path = str(tmp_path / "snap.safetensors")
+    qkv.save_prompt_cache(path, caches, {"model": "flint"})
+    with safe_open(path, "pt") as f:
+        meta = f.metadata()
+        assert f.get_tensor("0.0.0").dtype == torch.uint32 and f.get_tensor("1.1.2").shape == (1, 2, 17, 2)
+    assert meta["0.0.1"] == "300" and meta["0.1.1"] == "17" and meta["0.0.0"] == "256" and meta["0.0.3"] == "8"
+    assert meta["1.model"] == "flint" and meta["2.0"] == meta["2.1"] == "QuantizedKVCache8"
+    back, md = qkv.load_prompt_cache(path, device="cpu", return_metadata=True)
+    assert md == {"model": "flint"} and [c.offset for c in back] == [300, 17]
+    for c0, c1 in zip(caches, back):
+        for a, x in zip(c0.state[0] + c0.state[1], c1.keys + c1.values):
+            assert a.dtype == x.dtype and torch.equal(a, x)
+    qkv.save_prompt_cache(path, caches[:1])  # no metadata
+    assert qkv.load_prompt_cache(path, device="cpu")[0].offset == 300

@@ -364,3 +364,41 @@ def test_c_sdpa_matches_float64_oracle(mask):
         got8 = cbind.sdpa_q8(q16, K, V, 0.0884, mask, s16, n=N, start=start, **kw)
         ref8 = oa.sdpa_q8(q16, K, V, 0.0884, vis[:, None], s16, n=N)
         assert np.abs(got8 - ref8).max() < 2e-6
+
+
+def _triple(B, KVH, cap, seed):
+    g = np.random.default_rng(seed)
+    return (g.integers(0, 2 ** 32, (B, KVH, cap, 32), dtype=np.uint32),
+            g.integers(0, 2 ** 16, (B, KVH, cap, 2), dtype=np.uint16),
+            g.integers(0, 2 ** 16, (B, KVH, cap, 2), dtype=np.uint16))
+
+
+def test_cache_row_bookkeeping_oracle():
+    """oracle.cache against positions worked out by hand from locals/qkv.py:340-440: requests of 20 and 11 keys
+    merge right-aligned; extend with a 30-key request pads the older rows by 10; filter drops the shared padding;
+    extract returns a row's own keys; finalize rolls rows right by their right padding; growth keeps prev and
+    appends whole steps."""
+    from oracle import cache as oc
+
+    t1, t2, t3 = _triple(1, 2, 256, 1), _triple(1, 2, 256, 2), _triple(1, 2, 64, 3)
+    b = oc.merge([(t1, 20), (t2, 11), (None, 0)], KVH=2)
+    assert b["idx"] == 20 and b["left_padding"].tolist() == [0, 9, 20] and b["offset"].tolist() == [20, 11, 0]
+    for a, x in zip(b["keys"], t2):
+        assert np.array_equal(a[1, :, 9:20], x[0, :, :11]) and not a[1, :, :9].any() and not a[2].any()
+    e, n = oc.extract(b, 1)
+    assert n == 11 and all(np.array_equal(a[0], x[0, :, :11]) for a, x in zip(e, t2))
+    b3 = oc.merge([(t3, 30)], KVH=2)
+    x = oc.extend(b, b3, KVH=2)
+    assert x["idx"] == 30 and x["left_padding"].tolist() == [10, 19, 30, 0] and x["keys"][0].shape[2] == 30
+    for a, y in zip(x["keys"], t1):
+        assert np.array_equal(a[0, :, 10:30], y[0, :, :20]) and not a[0, :, :10].any()
+    f = oc.filter_rows(x, [1, 0])
+    assert f["idx"] == 20 and f["left_padding"].tolist() == [9, 0] and f["keys"][0].shape[2] == 20
+    for a, y in zip(f["keys"], t1):
+        assert np.array_equal(a[1, :, :20], y[0, :, :20])
+    r = oc.finalize({"keys": tuple(a[:, :, :5] for a in t1), "left_padding": np.array([0]), "offset": np.array([5]),
+                     "idx": 5}, [2])
+    assert r["left_padding"].tolist() == [2] and r["offset"].tolist() == [3]
+    assert np.array_equal(r["keys"][0][0, 0, :, 0], t1[0][0, 0, [3, 4, 0, 1, 2], 0])
+    g = oc.grow(tuple(a[:, :, :700] for a in _triple(2, 2, 700, 4)), 700, 1, KVH=2, B=2)
+    assert g[0].shape[2] == 956 and not g[0][:, :, 700:].any()
