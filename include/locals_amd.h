@@ -179,7 +179,7 @@ int lcl_sdpa_ex(const void* q, int qdt, int kvfmt, const uint32_t* kw, const voi
 /* qk_kernel.qk_norm_rope (locals/qk_kernel.py:24-109, metal_kernel source
  * :24-69, launch :85-109): per-head RMS norms of q and k, RoPE over halves, v
  * split out.
- *   qkv  (B, L, (H + 2 KV) * head_dim) dtype dt (f16 or bf16); head_dim 128, 256 or 512
+ *   qkv  (B, L, (H + 2 KV) * head_dim) dtype dt (f16 or bf16); head_dim a multiple of 128 up to 1024
  *   q_w, k_w (head_dim,) dtype dt: the q_norm / k_norm weights; eps the shared norm eps
  *   offsets int32 device array: (B,) if offsets_per_row else (1,); position of
  *     (b, l) is offsets[b or 0] + l

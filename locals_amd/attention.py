@@ -29,8 +29,9 @@ def ragged_attention(q: torch.Tensor, keys: torch.Tensor, values: torch.Tensor, 
     n_slots, Hkv, cap, D2 = keys.shape
     if D2 != D:
         raise ValueError("head dims differ")
-    if D % 32 or H % Hkv:
-        raise ValueError("D must be a multiple of 32 and H a multiple of Hkv (locals/attention.py preconditions)")
+    if D % 32 or D > 512 or H % Hkv:
+        raise ValueError("D must be a multiple of 32 (at most 512) and H a multiple of Hkv (locals/attention.py "
+                         "preconditions)")
     if keys.dtype not in (torch.float16, torch.bfloat16) or values.dtype != keys.dtype:
         raise ValueError("keys/values must be float16 or bfloat16")
     if slots.numel() != R or nkeys.numel() != R:

@@ -1603,11 +1603,20 @@ int lcl_ragged_attention_ex(const void* q, int qdt, const void* keys, const void
                             size_t workspace_bytes, void* stream_, void* ev_start, void* ev_stop) {
   hipStream_t stream = static_cast<hipStream_t>(stream_);
   if (!q || !keys || !values || !slots || !nkeys || !out) return -1;
-  if (hd != kHD) return -2;
+  if (hd != kHD && !generic_head_dim_ok(hd, false)) return -2;
   if (R < 0 || H <= 0 || Hkv <= 0 || H % Hkv || n_slots <= 0 || cap <= 0) return -1;
   if (block < 0 || block % 64) return -1;
   if ((qdt != DT_F16 && qdt != DT_BF16 && qdt != DT_F32) || (kvdt != DT_F16 && kvdt != DT_BF16)) return -1;
   if (R == 0) return 0;
+  if (hd != kHD) {  // other head sizes: the generic kernel (no split, no workspace)
+    GenParams g{};
+    g.q = q; g.qdt = qdt; g.kvfmt = 1; g.kf = keys; g.vf = values; g.kvdt = kvdt;
+    g.slots = slots; g.nkeys = nkeys; g.mask = 0;
+    g.scale = scale; g.scale_dev = scale_dev;
+    g.R = R; g.H = H; g.KVH = Hkv; g.L = 1; g.N = cap; g.D = hd; g.cap = cap; g.kv_rows = n_slots;
+    g.out = out; g.odt = qdt;
+    return attn_generic_launch(g, stream);
+  }
   const int chunk = pick_chunk(block, cap);
   const int nchunks = (cap + chunk - 1) / chunk;
   if (!workspace || workspace_bytes < ws_bytes_for(R, H, nchunks)) return -3;

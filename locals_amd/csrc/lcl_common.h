@@ -222,6 +222,40 @@ __device__ __forceinline__ void lds_load4(BufRsrc r, void* lds, uint32_t voff) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)(lds), 4, voff, 0, 0, AUX);
 }
 
+// generic.hip: attention for head sizes other than 128 (every mask kind, 16-bit or 8-bit K/V, ragged rows)
+struct GenParams {
+  const void* q;  // (R, H, L, D), dtype qdt
+  int qdt;
+  int kvfmt;  // 0: 8-bit triples, 1: 16-bit
+  const void* kf;
+  const void* vf;  // 16-bit (kv_rows, KVH, cap, D), dtype kvdt
+  const uint32_t* kw;
+  const void* ks;
+  const void* kb;
+  const uint32_t* vw;
+  const void* vs;
+  const void* vb;  // 8-bit: words (kv_rows, KVH, cap, D / 4), scales / biases (.., D / 64) of dtype kvdt
+  int kvdt;
+  const int32_t* slots;  // KV row of each query row, or null (row r)
+  const int32_t* start;  // first key of each row, or null
+  const int32_t* nkeys;  // end of each row's keys, or null (N)
+  int mask, window;
+  const unsigned long long* tree;
+  long long tree_bs;
+  const uint8_t* dense;
+  long long msb, msh, msq, msk;
+  const float* sinks;  // (H,) natural log units, or null
+  float scale;
+  const float* scale_dev;
+  int R, H, KVH, L, N, D, cap, kv_rows;
+  void* out;
+  int odt;
+};
+
+int attn_generic_launch(const GenParams& p, hipStream_t stream);
+// head sizes it takes: a multiple of 16 up to 512 (16-bit K/V), of 64 (8-bit)
+inline bool generic_head_dim_ok(int D, bool q8) { return D > 0 && D <= 512 && D % (q8 ? 64 : 16) == 0; }
+
 // quant.hip: K and V (rows of 128 values) of an 8-bit cache dequantized to the scales' 16-bit dtype in one launch
 int dequantize_kv128(const uint32_t* kw, const void* ks, const void* kb, const uint32_t* vw, const void* vs,
                      const void* vb, int sdt, long long rows, void* kout, void* vout, hipStream_t stream);

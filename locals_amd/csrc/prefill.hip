@@ -788,7 +788,7 @@ int lcl_sdpa_ex(const void* q, int qdt, int kvfmt, const uint32_t* kw, const voi
                 void* workspace, size_t workspace_bytes, void* stream_, void* ev_start, void* ev_stop) {
   hipStream_t stream = static_cast<hipStream_t>(stream_);
   if (!q || !out) return -1;
-  if (head_dim != kD) return -2;
+  if (head_dim != kD && !generic_head_dim_ok(head_dim, kvfmt == KV_Q8)) return -2;
   if (B <= 0 || H <= 0 || KVH <= 0 || H % KVH || L <= 0 || N < 0 || N > cap || cap <= 0 || L > N + 1000000) return -1;
   if (block < 0 || block % kKT) return -1;
   if (qdt != DT_F16 && qdt != DT_BF16 && qdt != DT_F32) return -1;
@@ -805,6 +805,21 @@ int lcl_sdpa_ex(const void* q, int qdt, int kvfmt, const uint32_t* kw, const voi
   if (mask_kind == MK_WINDOW && window <= 0) return -1;
   if (mask_kind == MK_TREE && (!tree || L > 64 || L > N)) return -2;
   if (mask_kind == MK_DENSE && !dense) return -1;
+  if (head_dim != kD) {  // other head sizes: the generic kernel (no split, no workspace)
+    GenParams g{};
+    g.q = q; g.qdt = qdt; g.kvfmt = kvfmt; g.kf = kf; g.vf = vf;
+    g.kw = kw; g.ks = ks; g.kb = kb; g.vw = vw; g.vs = vs; g.vb = vb; g.kvdt = kvdt;
+    g.start = start; g.mask = mask_kind; g.window = window; g.tree = tree; g.tree_bs = tree_bs;
+    g.dense = dense; g.msb = msb; g.msh = msh; g.msq = msq; g.msk = msk;
+    g.sinks = sinks; g.scale = scale;
+    g.R = B; g.H = H; g.KVH = KVH; g.L = L; g.N = N; g.D = head_dim; g.cap = cap; g.kv_rows = B;
+    g.out = out; g.odt = qdt;
+    hipEvent_t e0 = static_cast<hipEvent_t>(ev_start), e1 = static_cast<hipEvent_t>(ev_stop);
+    if (e0) hipEventRecord(e0, stream);
+    const int rc = attn_generic_launch(g, stream);
+    if (e1) hipEventRecord(e1, stream);
+    return rc;
+  }
   const int rows = L * (H / KVH);
   const int rt = sdpa_row_tiles(rows, mask_kind, kvfmt);
   int chunk = sdpa_chunk(block, B, H, L, N, 64 * rt);

@@ -256,18 +256,25 @@ static void launch_rope(bool rope, const QkParams& p, hipStream_t s) {
   else hipLaunchKernelGGL((qk_norm_rope_k<DT, PER, false, FUSED>), grid, dim3(256), 0, s, p);
 }
 
+template <int DT, bool FUSED>
+static void launch_per(int per, bool rope, const QkParams& p, hipStream_t s) {
+  switch (per) {
+    case 1: launch_rope<DT, 1, FUSED>(rope, p, s); break;
+    case 2: launch_rope<DT, 2, FUSED>(rope, p, s); break;
+    case 3: launch_rope<DT, 3, FUSED>(rope, p, s); break;
+    case 4: launch_rope<DT, 4, FUSED>(rope, p, s); break;
+    case 5: launch_rope<DT, 5, FUSED>(rope, p, s); break;
+    case 6: launch_rope<DT, 6, FUSED>(rope, p, s); break;
+    case 7: launch_rope<DT, 7, FUSED>(rope, p, s); break;
+    default: launch_rope<DT, 8, FUSED>(rope, p, s); break;
+  }
+}
+
 template <bool FUSED>
 static int launch_qk(int dt, int head_dim, bool rope, const QkParams& p, hipStream_t s) {
   const int per = head_dim / 128;
-  if (dt == DT_F16) {
-    if (per == 1) launch_rope<DT_F16, 1, FUSED>(rope, p, s);
-    else if (per == 2) launch_rope<DT_F16, 2, FUSED>(rope, p, s);
-    else launch_rope<DT_F16, 4, FUSED>(rope, p, s);
-  } else {
-    if (per == 1) launch_rope<DT_BF16, 1, FUSED>(rope, p, s);
-    else if (per == 2) launch_rope<DT_BF16, 2, FUSED>(rope, p, s);
-    else launch_rope<DT_BF16, 4, FUSED>(rope, p, s);
-  }
+  if (dt == DT_F16) launch_per<DT_F16, FUSED>(per, rope, p, s);
+  else launch_per<DT_BF16, FUSED>(per, rope, p, s);
   return int(hipGetLastError());
 }
 
@@ -275,7 +282,7 @@ static int launch_qk(int dt, int head_dim, bool rope, const QkParams& p, hipStre
 static int check_dims(int dt, int B, int L, int H, int KV, int head_dim) {
   if (dt != DT_F16 && dt != DT_BF16) return LCL_EUNSUPPORTED;
   if (B < 0 || L < 0 || H <= 0 || KV <= 0 || H % KV) return LCL_EINVAL;
-  if (head_dim != 128 && head_dim != 256 && head_dim != 512) return LCL_EUNSUPPORTED;
+  if (head_dim <= 0 || head_dim % 128 || head_dim > 1024) return LCL_EUNSUPPORTED;  // 128 x (1 .. 8)
   if ((long long)B * L > 0x7fffffffLL) return LCL_EINVAL;
   return 0;
 }

@@ -22,7 +22,7 @@ from .qkv import _round_code, quantized
 
 USE_QK_KERNEL = os.environ.get("LOCALS_QK_KERNEL", "1") != "0"
 
-HEAD_DIMS = (128, 256, 512)  # the head sizes the kernel is built for
+HEAD_DIMS = tuple(128 * k for k in range(1, 9))  # the head sizes the kernel is built for: multiples of 128 to 1024
 
 
 def fits(attn, qkv: torch.Tensor) -> bool:

@@ -109,22 +109,23 @@ def _kv_view(t: torch.Tensor, name: str):
 
 def scaled_dot_product_attention(q: torch.Tensor, k, v, *, scale: float, mask=None,
                                  sinks: Optional[torch.Tensor] = None, start: Optional[torch.Tensor] = None):
-    """Attention of ``q`` (B, H, L, 128) over ``k``/``v`` -- (B, KVH, N, 128) fp16/bf16 tensors, or 8-bit
+    """Attention of ``q`` (B, H, L, D) over ``k``/``v`` -- (B, KVH, N, D) fp16/bf16 tensors, or 8-bit
     (words, scales, biases) triples of N positions -- with MLX's mask and sink semantics.  ``start`` (B,) masks the
-    keys before start[b] (a left-padded batch).  Returns (B, H, L, 128) in q's dtype."""
+    keys before start[b] (a left-padded batch).  Returns (B, H, L, D) in q's dtype.  D = 128 runs on the tiled MFMA
+    kernels; other head sizes (a multiple of 16 up to 512 for 16-bit K/V, of 64 for 8-bit) on a general kernel."""
     if q.dim() != 4:
         raise ValueError("q must be (B, H, L, D)")
     B, H, L, D = q.shape
-    if D != 128:
-        raise ValueError("head_dim 128 only (the kernels' layout)")
     q8 = isinstance(k, (tuple, list))
+    if not (0 < D <= 512 and D % (64 if q8 else 16) == 0):
+        raise ValueError(f"head_dim {D} not supported (a multiple of {64 if q8 else 16} up to 512)")
     if q8:
         kt = tuple(_kv_view(a, "keys") for a in k)
         vt = tuple(_kv_view(a, "values") for a in v)
         kw, ks, kb = (a for a, _ in kt)
         vw, vs, vb = (a for a, _ in vt)
-        if not _words_ok(kw) or kw.shape[3] * 4 != D:
-            raise ValueError("8-bit keys must be (B, KVH, N, 32) words with scales/biases (B, KVH, N, 2)")
+        if not _words_ok(kw) or kw.shape[3] * 4 != D or ks.shape[3] * 64 != D:
+            raise ValueError("8-bit keys must be (B, KVH, N, D / 4) words with scales/biases (B, KVH, N, D / 64)")
         caps = {c for _, c in kt + vt}
         if len(caps) != 1:
             raise ValueError("8-bit buffers of different capacities")

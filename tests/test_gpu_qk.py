@@ -56,6 +56,8 @@ CASES = [  # B, L, H, KV, HD, offset
     (1, 64, 32, 8, 128, 16384),
     (2, 5, 4, 2, 256, [-3, 9000]),
     (1, 3, 2, 1, 512, 7),
+    (2, 2, 2, 1, 384, [11, 2048]),
+    (1, 2, 2, 2, 1024, 5),
 ]
 
 
