@@ -339,15 +339,26 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
           kin ? make_uint4(o[4 * u], o[4 * u + 1], o[4 * u + 2], o[4 * u + 3]) : make_uint4(0u, 0u, 0u, 0u);
   };
 
-  float m_run[RT], l_acc[RT];
+  // Softmax state of this lane's row in each row tile: the lazy running max m_run (moved only when a tile's max
+  // passes it by kThr, so p <= 2^kThr), negm = -m_run broadcast (0 before the first key), the C operand the
+  // Q K^T chain starts from, so the scores come out as s - m_run and need no subtraction before exp2, and the
+  // threshold a tile's max is checked against (kThr, or -inf before the first key).  The denominator is summed on
+  // MFMA as P^T times a ones operand (Lacc: every lane gets its row's sum of exactly the rounded P that multiplies
+  // V, so the weights of the output are consistent), rescaled with O.
+  float m_run[RT], thr[RT];
+  f4 negm[RT], Lacc[RT];
   f4 O[RT][8];
 #pragma unroll
   for (int r = 0; r < RT; r++) {
     m_run[r] = -INFINITY;
-    l_acc[r] = 0.0f;
+    thr[r] = -INFINITY;
+    negm[r] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+    Lacc[r] = f4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int dd = 0; dd < 8; dd++) O[r][dd] = f4{0.0f, 0.0f, 0.0f, 0.0f};
   }
+  const uint32_t one2 = MT == DT_BF16 ? 0x3f803f80u : 0x3c003c00u;  // two 1.0 of the MFMA type
+  const uint4 ones = make_uint4(one2, one2, one2, one2);
   // per-row mask state
   unsigned long long tbits[RT];
   const uint8_t* drow[RT];
@@ -401,11 +412,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     // tile), the 32-dim step kk is the outer loop, so the 4 RT accumulators are independent chains and a step's
     // four K fragments are read together; otherwise a key block t at a time.
     constexpr bool kStepOuter = MASK == MK_CAUSAL || RT == 1;
-    f4 st[RT][4];
-#pragma unroll
-    for (int t = 0; t < 4; t++)
-#pragma unroll
-      for (int r = 0; r < RT; r++) st[r][t] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+    f4 st[RT][4];  // relative to m_run: every chain starts from negm
     // a tile every key of which every row of the wave sees needs no mask (for causal prefill, all but the
     // diagonal tiles); rows past the row count are not written, so they need none either
     bool full = t0 >= klo && t0 + kKT <= khi;
@@ -416,8 +423,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
              t0 > p.N - p.L + (row0 + 64 * (RT - 1) + 16 * wave + 15) / p.G - p.window;
     if constexpr (MASK == MK_DENSE) full = false;
     if constexpr (kStepOuter) {
-      // The mask enters as the accumulators' initial value (0 or -inf), so the scores need no pass after the
-      // products and a full tile's first step takes the constant 0.  Every key row of the tile is finite: rows
+      // The mask enters as the accumulators' initial value (-m_run or -inf), so the scores need no pass after the
+      // products and a full tile's first step takes negm as it is.  Every key row of the tile is finite: rows
       // outside [klo, khi) were cleared in the slot (16-bit) or dequantized as 0 (8-bit).
       uint4 kf[4];
 #pragma unroll
@@ -426,14 +433,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
         for (int t = 0; t < 4; t++)
 #pragma unroll
-          for (int r = 0; r < RT; r++) st[r][t] = mma32<MT>(kf[t], qb[r][0], st[r][t]);
+          for (int r = 0; r < RT; r++) st[r][t] = mma32<MT>(kf[t], qb[r][0], negm[r]);
       } else {
 #pragma unroll
         for (int r = 0; r < RT; r++)
 #pragma unroll
           for (int t = 0; t < 4; t++)
 #pragma unroll
-            for (int i = 0; i < 4; i++) st[r][t][i] = key_visible(r, t0 + 16 * t + 4 * q4 + i) ? 0.0f : -INFINITY;
+            for (int i = 0; i < 4; i++)
+              st[r][t][i] = key_visible(r, t0 + 16 * t + 4 * q4 + i) ? negm[r][0] : -INFINITY;
 #pragma unroll
         for (int t = 0; t < 4; t++)
 #pragma unroll
@@ -455,7 +463,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         for (int kk = 0; kk < 4; kk++) {
           const uint4 kf = kfrag(S, t, kk);
 #pragma unroll
-          for (int r = 0; r < RT; r++) st[r][t] = mma32<MT>(kf, qb[r][kk], st[r][t]);
+          for (int r = 0; r < RT; r++) st[r][t] = mma32<MT>(kf, qb[r][kk], kk ? st[r][t] : negm[r]);
         }
     }
     uint4 pb[RT][2];  // P^T as B operands: k index 8 q4 + j <-> key 32 u + (j < 4 ? 4 q4 + j : 16 + 4 q4 + j - 4)
@@ -477,32 +485,32 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
           }
         }
       }
-      tmax = max_x32(max_x16(tmax));
-      if (tmax > m_run[r] + kThr) {  // lane-local rescale (O^T rows live in this lane column)
-        const float corr = m_run[r] == -INFINITY ? 0.0f : fast_exp2(m_run[r] - tmax);
-        m_run[r] = tmax;
-        l_acc[r] *= corr;
+      tmax = max_x32(max_x16(tmax));  // relative to m_run (absolute before the first key)
+      if (tmax > thr[r]) {  // lane-local rescale (O^T rows live in this lane column)
+        const float corr = m_run[r] == -INFINITY ? 0.0f : fast_exp2(-tmax);
+        m_run[r] = m_run[r] == -INFINITY ? tmax : m_run[r] + tmax;
+        negm[r] = f4{-m_run[r], -m_run[r], -m_run[r], -m_run[r]};
+        thr[r] = kThr;
+        Lacc[r] *= corr;
 #pragma unroll
         for (int dd = 0; dd < 8; dd++) O[r][dd] *= corr;
+#pragma unroll
+        for (int t = 0; t < 4; t++) st[r][t] -= f4{tmax, tmax, tmax, tmax};
       }
-      // a row that has seen no key yet (m_run -inf) has only -inf scores here: exp2(-inf - 0) = 0
-      const float msub = m_run[r] == -INFINITY ? 0.0f : m_run[r];
+      // scores are relative to m_run; a row that has seen no key yet has only -inf here: exp2(-inf) = 0
       uint32_t pw[4][2];
 #pragma unroll
       for (int t = 0; t < 4; t++) {
         float pv[4];
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-          pv[i] = fast_exp2(st[r][t][i] - msub);  // -inf -> 0
-          l_acc[r] += pv[i];
-        }
+        for (int i = 0; i < 4; i++) pv[i] = fast_exp2(st[r][t][i]);  // -inf -> 0
         pw[t][0] = pack2<MT>(pv[0], pv[1]);
         pw[t][1] = pack2<MT>(pv[2], pv[3]);
       }
       pb[r][0] = make_uint4(pw[0][0], pw[0][1], pw[1][0], pw[1][1]);
       pb[r][1] = make_uint4(pw[2][0], pw[2][1], pw[3][0], pw[3][1]);
     }
-    // O^T += V^T P^T, 32 keys a step
+    // O^T += V^T P^T, 32 keys a step; the denominator as ones times P^T
 #pragma unroll
     for (int u = 0; u < 2; u++) {
 #pragma unroll
@@ -511,6 +519,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
         for (int r = 0; r < RT; r++) O[r][dd] = mma32<MT>(vf, pb[r][u], O[r][dd]);
       }
+#pragma unroll
+      for (int r = 0; r < RT; r++) Lacc[r] = mma32<MT>(ones, pb[r][u], Lacc[r]);
     }
   };
 
@@ -606,11 +616,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     }
   }
 
-  // ---- each row's part: m, l (summed over the 4 lanes of the row), o[dims]
+  // ---- each row's part: m, l, o[dims]
 #pragma unroll
   for (int r = 0; r < RT; r++) {
-    float l = l_acc[r];
-    l = add_x32(add_x16(l));
+    const float l = Lacc[r][0];  // every lane of the row holds the whole sum
     if (!real[r]) continue;
     if (p.direct) {  // the only chunk: join with the sink here, as sdpa_combine would
       const size_t row = (size_t(b) * p.H + head[r]) * p.L + qi[r];
@@ -815,9 +824,9 @@ int lcl_sdpa_ex(const void* q, int qdt, int kvfmt, const uint32_t* kw, const voi
     g.R = B; g.H = H; g.KVH = KVH; g.L = L; g.N = N; g.D = head_dim; g.cap = cap; g.kv_rows = B;
     g.out = out; g.odt = qdt;
     hipEvent_t e0 = static_cast<hipEvent_t>(ev_start), e1 = static_cast<hipEvent_t>(ev_stop);
-    if (e0) hipEventRecord(e0, stream);
+    if (e0) (void)hipEventRecord(e0, stream);
     const int rc = attn_generic_launch(g, stream);
-    if (e1) hipEventRecord(e1, stream);
+    if (e1) (void)hipEventRecord(e1, stream);
     return rc;
   }
   const int rows = L * (H / KVH);
@@ -841,7 +850,7 @@ int lcl_sdpa_ex(const void* q, int qdt, int kvfmt, const uint32_t* kw, const voi
   if (dq) {
     _Float16* kd = reinterpret_cast<_Float16*>(static_cast<uint8_t*>(workspace) + align256(need));
     _Float16* vd = kd + size_t(B) * KVH * cap * kD;
-    if (e0) hipEventRecord(e0, stream);
+    if (e0) (void)hipEventRecord(e0, stream);
     const int rc = dequantize_kv128(kw, ks, kb, vw, vs, vb, kvdt, (long long)B * KVH * cap, kd, vd, stream);
     if (rc) return rc;
     kvfmt = KV_16;
@@ -874,7 +883,7 @@ int lcl_sdpa_ex(const void* q, int qdt, int kvfmt, const uint32_t* kw, const voi
     const dim3 grid(unsigned((total + 7) / 8 * 8));
     if (kvfmt == KV_Q8) launch_fmt<KV_Q8>(qdt, kvdt, rt, grid, stream, e0, e1, p);
     else launch_fmt<KV_16>(qdt, kvdt, rt, grid, stream, e0, e1, p);
-    if (dq_stop) hipEventRecord(dq_stop, stream);
+    if (dq_stop) (void)hipEventRecord(dq_stop, stream);
   }
   if (!p.direct) {
     SdpaCombineParams c{p.pm, p.pl, p.po, sinks, out, B * H * L, H, L, nchunks, qdt};
