@@ -164,16 +164,22 @@ __device__ __forceinline__ void split_bf2(float a, float b, uint32_t& hi, uint32
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Maximum of floats as v_maximum3_f32 (NaN-propagating).  fmaxf's IEEE maxNum needs quieted inputs, so the
+// compiler puts a v_max_f32 x, x, x before each operand it cannot prove canonical (every MFMA result): one extra
+// VALU per score.  The scores compared here hold no NaN, so the two agree on them.
+__device__ __forceinline__ float vmax(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+__device__ __forceinline__ float vmax3(float a, float b, float c) { return vmax(vmax(a, b), c); }
+
 // Max / sum of a value with lane l ^ 16 (or l ^ 32) of the wave on gfx950's v_permlane16_swap / v_permlane32_swap:
 // VALU lane exchanges instead of an LDS-routed shuffle.  With both operands x, lane l gets x of lanes l and l ^ 16
 // (l ^ 32) in some order (checked in bounds on an MI355X), so a commutative op gives the xor shuffle's result.
 __device__ __forceinline__ float max_x16(float x) {
   const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  return vmax(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 __device__ __forceinline__ float max_x32(float x) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  return vmax(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 __device__ __forceinline__ float add_x16(float x) {
   const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);

@@ -470,10 +470,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
     for (int r = 0; r < RT; r++) {
       float tmax = -INFINITY;
-      if (kStepOuter || full) {
-#pragma unroll
-        for (int t = 0; t < 4; t++)
-          tmax = fmaxf(tmax, fmaxf(fmaxf(st[r][t][0], st[r][t][1]), fmaxf(st[r][t][2], st[r][t][3])));
+      if (kStepOuter || full) {  // 16 scores in eight 3-input maxima
+        const f4 *a = st[r];
+        const float x0 = vmax3(a[0][0], a[0][1], a[0][2]), x1 = vmax3(a[0][3], a[1][0], a[1][1]);
+        const float x2 = vmax3(a[1][2], a[1][3], a[2][0]), x3 = vmax3(a[2][1], a[2][2], a[2][3]);
+        const float x4 = vmax3(a[3][0], a[3][1], a[3][2]);
+        tmax = vmax(vmax3(x0, x1, x2), vmax3(x3, x4, a[3][3]));
       } else {
 #pragma unroll
         for (int t = 0; t < 4; t++) {
@@ -481,7 +483,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
           for (int i = 0; i < 4; i++) {
             const float sc = key_visible(r, t0 + 16 * t + 4 * q4 + i) ? st[r][t][i] : -INFINITY;
             st[r][t][i] = sc;
-            tmax = fmaxf(tmax, sc);
+            tmax = vmax(tmax, sc);
           }
         }
       }
