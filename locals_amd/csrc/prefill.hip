@@ -47,11 +47,14 @@ constexpr int kKT = 64;                 // keys a tile
 constexpr int kKsStride = 144;
 constexpr int kRawSlot = 8192 + 8192 + 1024;  // an 8-bit raw tile: K codes, V codes, ks / kb / vs / vb
 constexpr float kThr = 6.0f;
-// A 16-bit K + V tile (64 key rows of 256 B each).  Key row r keeps its 16-byte chunk c at slot c ^ sw16(r), a
-// permutation of r's low four bits: the K operand reads (16 rows, one chunk each) are then free of bank
-// conflicts and the transposing V reads (16 consecutive rows, two chunks each) two-way, the least for 512 B.
+// A 16-bit K + V tile (64 key rows of 256 B each).  K row r keeps its 16-byte chunk c at slot c ^ swk(r), V row
+// r at slot c ^ swv(r).  Chosen by measuring each operand read pattern alone on an MI355X (8 waves a CU; B/clk
+// a workgroup): the K reads (lane c16 + 16 q4 takes chunk 4 kk + q4 of row c16) reach the 128 of a contiguous
+// read with swk, 85 with the swizzle that maps rows 0..3 to even chunks only; the transposing V reads (chunks
+// 2 d, 2 d + 1 of 16 consecutive rows, four lanes a row) 112 with swv against 85 with that one or with swk.
 constexpr int kRaw16 = 2 * kKT * kD * 2;
-__device__ __forceinline__ int sw16(int r) { return ((r << 1) & 6) | (r & 8) | ((r >> 2) & 1); }
+__device__ __forceinline__ int swk(int r) { return r & 15; }
+__device__ __forceinline__ int swv(int r) { return ((r & 7) << 1) | ((r >> 3) & 1); }
 
 enum MaskKind { MK_NONE = 0, MK_CAUSAL = 1, MK_TREE = 2, MK_DENSE = 3, MK_WINDOW = 4 };
 enum KvFmt { KV_Q8 = 0, KV_16 = 1 };
@@ -209,7 +212,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   // 8-bit: raw tiles arrive by direct buffer->LDS loads into two named slots (one in flight while the other is
   // staged) and are dequantized into one operand buffer (Ks; Vk key-major as the 16-bit V region, read through the
   // transposing read).  16-bit: the K and V tiles arrive the same way
-  // (chunks swizzled by sw16) and are the MFMA operands themselves -- K rows read as they are, V^T through the
+  // (chunks swizzled by swk / swv) and are the MFMA operands themselves -- K rows read as they are, V^T through the
   // transposing read -- so nothing is staged.
   __shared__ __attribute__((aligned(16))) uint16_t Ks[FMT == KV_Q8 ? kKT * kKsStride : 8];
   __shared__ __attribute__((aligned(16))) uint8_t Vk[FMT == KV_Q8 ? kKT * 256 : 16];
@@ -319,7 +322,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     }
   };
   // dequantize an 8-bit tile into the operand buffers: K rows into Ks, V rows into Vk (16-byte chunk c of key r at
-  // slot c ^ sw16(r)); keys outside [klo, khi) become 0 (MASKED: the tile straddles an end of the range;
+  // slot c ^ swv(r)); keys outside [klo, khi) become 0 (MASKED: the tile straddles an end of the range;
   // otherwise every key is inside and no test is made)
   auto stage = [&](int t0, const RawTile& T, auto masked) __attribute__((always_inline)) {
     constexpr bool MASKED = decltype(masked)::value;
@@ -332,7 +335,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     for (int u = 0; u < 4; u++)
       kdst[u] = kin ? make_uint4(o[4 * u], o[4 * u + 1], o[4 * u + 2], o[4 * u + 3]) : make_uint4(0u, 0u, 0u, 0u);
     dequant(T.v, T.vs, T.vb, o);
-    const int sw = sw16(kkey);
+    const int sw = swv(kkey);
 #pragma unroll
     for (int u = 0; u < 4; u++)
       *reinterpret_cast<uint4*>(&Vk[kkey * 256 + 16 * ((4 * kpart + u) ^ sw)]) =
@@ -374,8 +377,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   // K: key 16 t + c16, dims 32 kk + 8 q4 .. +7 (one 16-byte chunk); V^T: lane (g = q4, m = c16) points the
   // transposing read at key 32 u + 4 g + m / 4 (and + 16 for the second half), dims 16 dd + 4 (m % 4) .. +3, so
   // its 8 values are dim 16 dd + m of the keys whose P^T the B operand holds at k = 8 q4 + j.
-  const int sk16 = sw16(c16);
-  const int vkey16 = 4 * q4 + (c16 >> 2), vsw16 = sw16(vkey16);
+  const int sk16 = swk(c16);
+  const int vkey16 = 4 * q4 + (c16 >> 2), vsw16 = swv(vkey16);
   const int vch16 = (c16 & 3) >> 1, voff16 = vkey16 * 256 + 8 * (c16 & 1);
   auto kfrag = [&](const uint8_t* S, int t, int kk) __attribute__((always_inline)) -> uint4 {
     if constexpr (FMT == KV_Q8)
@@ -563,7 +566,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     }
   } else {
     // 16-bit: wave w loads key rows 16 w .. 16 w + 15 of K and of V (4 instructions of 1 KB each), chunk c of
-    // row r to slot c ^ sw16(r)
+    // row r to slot c ^ swk(r) (K) or c ^ swv(r) (V)
     constexpr int kWaitOne = (0xF << 8) | (0x7 << 4) | 8;  // vmcnt(8): the other slot's loads may stay in flight
     constexpr int kWaitAll = (0xF << 8) | (0x7 << 4);
     constexpr int kWaitLds = (0x3 << 14) | (0x7 << 4) | 0xF;
@@ -577,9 +580,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
       for (int u = 0; u < 4; u++) {
         const int r = 16 * wave + 4 * u + (lane >> 4);
-        const uint32_t voff = uint32_t(t0 + r) * 256u + 16u * uint32_t((lane & 15) ^ sw16(r));
-        dma16(dk16, ls + 1024u * uint32_t(4 * wave + u), voff);
-        dma16(dv16, ls + 16384u + 1024u * uint32_t(4 * wave + u), voff);
+        const uint32_t voff = uint32_t(t0 + r) * 256u + 16u * uint32_t(lane & 15);
+        dma16(dk16, ls + 1024u * uint32_t(4 * wave + u), voff ^ (16u * uint32_t(swk(r))));
+        dma16(dv16, ls + 16384u + 1024u * uint32_t(4 * wave + u), voff ^ (16u * uint32_t(swv(r))));
       }
     };
     // a tile reaching past [klo, khi): the K and V rows of keys outside it are cleared (rows past n or before
