@@ -240,7 +240,8 @@ def bench_multi(cfg, args, dev, return_runner=False):
     nbytes = int(lib.lcl_sdpa_workspace_bytes_kv(Bp, H, KVH, L, N, cap, sdpa.BLOCK, 1 if W else 0, mk))
     if not sdpa.DEQUANTIZE_FIRST:
         nbytes = split
-    # with room for it the library dequantizes K/V once and runs the 16-bit kernel; its events then span both
+    # with room for it the library dequantizes K/V once and runs the 16-bit kernel; the events bracket pass 1 alone,
+    # the call time covers the dequantization, pass 1 and the join
     route = "dequantize K/V, 16-bit pass 1" if nbytes > split else ("16-bit pass 1" if W else "fused 8-bit pass 1")
     ws = torch.empty(nbytes // 4 + 1, dtype=torch.float32, device=dev)
     out = torch.empty((Bp, H, L, 128), dtype=torch.bfloat16 if W else torch.float16, device=dev)

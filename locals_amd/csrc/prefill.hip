@@ -855,7 +855,6 @@ int lcl_sdpa_ex(const void* q, int qdt, int kvfmt, const uint32_t* kw, const voi
   if (dq) {
     _Float16* kd = reinterpret_cast<_Float16*>(static_cast<uint8_t*>(workspace) + align256(need));
     _Float16* vd = kd + size_t(B) * KVH * cap * kD;
-    if (e0) (void)hipEventRecord(e0, stream);
     const int rc = dequantize_kv128(kw, ks, kb, vw, vs, vb, kvdt, (long long)B * KVH * cap, kd, vd, stream);
     if (rc) return rc;
     kvfmt = KV_16;
@@ -877,18 +876,12 @@ int lcl_sdpa_ex(const void* q, int qdt, int kvfmt, const uint32_t* kw, const voi
   p.nchunks = nchunks; p.chunk = chunk; p.mask = mask_kind; p.window = window;
   p.direct = nchunks == 1; p.out = out; p.odt = qdt;
   p.nrowblocks = (rows + 64 * rt - 1) / (64 * rt);
-  hipEvent_t dq_stop = nullptr;
-  if (dq) {  // the events span the dequantization and pass 1: the start went in before the dequantization
-    dq_stop = e1;
-    e0 = e1 = nullptr;
-  }
   {  // with no key in reach every workgroup records empty parts, so the combine needs no cleared workspace
     const long long total = (long long)nchunks * p.nrowblocks * B * KVH;  // one-dimensional, mapped per XCD
     if (total > (1LL << 30)) return -2;
     const dim3 grid(unsigned((total + 7) / 8 * 8));
     if (kvfmt == KV_Q8) launch_fmt<KV_Q8>(qdt, kvdt, rt, grid, stream, e0, e1, p);
     else launch_fmt<KV_16>(qdt, kvdt, rt, grid, stream, e0, e1, p);
-    if (dq_stop) (void)hipEventRecord(dq_stop, stream);
   }
   if (!p.direct) {
     SdpaCombineParams c{p.pm, p.pl, p.po, sinks, out, B * H * L, H, L, nchunks, qdt};
