@@ -46,6 +46,7 @@
 
 #include <hip/hip_ext.h>
 
+#include <stdio.h>
 #include <stdlib.h>
 
 #include <mutex>
@@ -80,6 +81,7 @@ struct DecodeParams {
   int kv_rows;  // rows of the KV buffers (B, or n_slots); a slot outside is clamped
   int R;        // query rows
   int qwaves, qmint;  // quad pass 1: waves launched, least tiles a wave
+  int qwa, qwb;       // quad pass 1: split weights of waves on even / odd XCDs
   float scale_log2;
   const float* scale_dev;  // if set, the scale is read from device memory (times log2 e in the kernel)
   int qdt, sdt;
@@ -95,6 +97,7 @@ struct CombineParams {
   const int32_t* nkeys;
   int n, cap, H, nchunks, chunk, odt;
   int quad, R, KVH, G, qwaves, qmint;  // quad: parts are the stream-K slots of the quad pass 1
+  int qwa, qwb;
 };
 
 __device__ __forceinline__ void row_range(const int32_t* start, const int32_t* nkeys, int n, int cap, int r, int& lo,
@@ -479,11 +482,28 @@ __device__ __forceinline__ uint32_t row_take2(uint32_t x0, uint32_t x1) {
 }
 
 // Stream-K split of the quad pass 1: the (row, kv head, 64-key tile) list in row-major order
-// (a row's tiles are the 64-aligned ones overlapping its keys [lo, hi)) is cut into W equal
-// ranges, W = min(waves launched, total / mint), so every wave gets >= mint tiles and one
-// resident round of waves finishes together whatever the row lengths.  A wave writes one
-// partial for each (row, kv head) stream its range touches, at slot
-// j = wave - (wave holding the stream's first tile); pass 2 recomputes the same split.
+// (a row's tiles are the 64-aligned ones overlapping its keys [lo, hi)) is cut into W ranges,
+// W <= min(waves launched, total / mint), so every wave gets >= mint tiles and one resident
+// round of waves finishes together whatever the row lengths.  The ranges are weighted by the
+// XCD a wave runs on: one-wave workgroups go to XCD w mod 8 in turn, so even w run on even
+// XCDs (weight a) and odd w on odd ones (weight b); the odd XCDs' waves have run ~5% slower
+// on every MI355X measured.  A wave writes one partial for each (row, kv head) stream its
+// range touches, at slot j = wave - (wave holding the stream's first tile); pass 2
+// recomputes the same split.
+__device__ __forceinline__ long long quad_prefix(int w, int a, int b) {
+  return (long long)((w + 1) / 2) * a + (long long)(w / 2) * b;
+}
+// first global tile of wave w
+__device__ __forceinline__ long long quad_start(int w, long long T, int W, int a, int b) {
+  return T * quad_prefix(w, a, b) / quad_prefix(W, a, b);
+}
+// wave count: the lightest share keeps >= mint tiles (floor(T min(a, b) / Q) <= any range's length)
+__device__ __forceinline__ int quad_wave_count(long long T, int wlaunch, int mint, int a, int b) {
+  int W = int(min((long long)wlaunch, max(1LL, T / mint)));
+  const int m = min(a, b);
+  while (W > 1 && T * m < (long long)mint * quad_prefix(W, a, b)) W--;
+  return W;
+}
 __device__ __forceinline__ int quad_row_tiles(const int32_t* start, const int32_t* nkeys, int n, int cap, int r,
                                               int& t0, int& lo, int& hi) {
   row_range(start, nkeys, n, cap, r, lo, hi);
@@ -515,7 +535,8 @@ __device__ __forceinline__ int wave_incl_scan(int x) {
 // total tiles T (all rows x KVH) and the wave count W of the split; with `row` >= 0 also the tiles of the rows
 // before it (`before`, in row units)
 __device__ __forceinline__ void quad_split(const int32_t* start, const int32_t* nkeys, int n, int cap, int R, int KVH,
-                                           int wlaunch, int mint, long long& T, int& W, int row, long long& before) {
+                                           int wlaunch, int mint, int a, int b, long long& T, int& W, int row,
+                                           long long& before) {
   const int lane = threadIdx.x & 63;
   long long t = 0;
   before = 0;
@@ -526,7 +547,7 @@ __device__ __forceinline__ void quad_split(const int32_t* start, const int32_t* 
     t += __shfl(incl, 63);
   }
   T = t * KVH;
-  W = int(min((long long)wlaunch, max(1LL, T / mint)));
+  W = quad_wave_count(T, wlaunch, mint, a, b);
 }
 
 // the row holding global tile g (0 <= g < T) and the global index of its first tile
@@ -561,8 +582,13 @@ __device__ __forceinline__ int quad_next_row(const int32_t* start, const int32_t
   return R;
 }
 
-// wave holding global tile g: the largest w with w T / W <= g
-__device__ __forceinline__ int quad_wave_of(long long g, long long T, int W) { return int(((g + 1) * W - 1) / T); }
+// wave holding global tile g (0 <= g < T): the largest w with quad_start(w) <= g, i.e. with
+// quad_prefix(w) <= X = floor(((g + 1) Q - 1) / T); the prefix grows by a, b, a, b, ...
+__device__ __forceinline__ int quad_wave_of(long long g, long long T, int W, int a, int b) {
+  const long long X = ((g + 1) * quad_prefix(W, a, b) - 1) / T;
+  const long long k = X / (a + b);
+  return int(2 * k + (X - k * (a + b) >= a ? 1 : 0));
+}
 
 // a (row, kv head) stream of the quad pass 1
 struct QStream {
@@ -626,10 +652,10 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void
     const int c = quad_lane_count(p.start, p.nkeys, p.n, p.cap, p.R, lane);
     const int incl = wave_incl_scan(c);
     T = uni((long long)__shfl(incl, 63) * p.KVH);
-    W = int(min((long long)p.qwaves, max(1LL, T / p.qmint)));
+    W = quad_wave_count(T, p.qwaves, p.qmint, p.qwa, p.qwb);
     if (wv >= W) return;
-    g = wv * T / W;
-    gend = (wv + 1) * T / W;
+    g = quad_start(wv, T, W, p.qwa, p.qwb);
+    gend = quad_start(wv + 1, T, W, p.qwa, p.qwb);
     if (g >= gend) return;
     const long long lo_t = (long long)(incl - c) * p.KVH, hi_t = (long long)incl * p.KVH;
     const unsigned long long m = __ballot(c > 0 && g >= lo_t && g < hi_t);
@@ -637,12 +663,12 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void
     row_first = uni((long long)__shfl(incl - c, r0) * p.KVH);
   } else {
     long long unused;
-    quad_split(p.start, p.nkeys, p.n, p.cap, p.R, p.KVH, p.qwaves, p.qmint, T, W, -1, unused);
+    quad_split(p.start, p.nkeys, p.n, p.cap, p.R, p.KVH, p.qwaves, p.qmint, p.qwa, p.qwb, T, W, -1, unused);
     T = uni(T);
     W = uni(W);
     if (wv >= W) return;
-    g = wv * T / W;
-    gend = (wv + 1) * T / W;
+    g = quad_start(wv, T, W, p.qwa, p.qwb);
+    gend = quad_start(wv + 1, T, W, p.qwa, p.qwb);
     if (g >= gend) return;
     r0 = uni(quad_locate(p.start, p.nkeys, p.n, p.cap, p.R, p.KVH, g, row_first));
     row_first = uni(row_first);
@@ -1020,7 +1046,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void
       wb1[e] += __shfl_xor(wb1[e], 16);
       wb1[e] += __shfl_xor(wb1[e], 32);
     }
-    const int jslot = wv - quad_wave_of(cur.Gs, T, W);
+    const int jslot = wv - quad_wave_of(cur.Gs, T, W, p.qwa, p.qwb);
     // lanes of quad q4 < HG write head group q4: row i of O is head 4 q4 + i
     if (q4 < HG) {
       const int e = HG == 1 ? 0 : q4;
@@ -1271,13 +1297,13 @@ __global__ __launch_bounds__(256) void decode_combine(CombineParams p) {
   if (p.quad) {
     long long T, before;
     int W;
-    quad_split(p.start, p.nkeys, p.n, p.cap, p.R, p.KVH, p.qwaves, p.qmint, T, W, r, before);
+    quad_split(p.start, p.nkeys, p.n, p.cap, p.R, p.KVH, p.qwaves, p.qmint, p.qwa, p.qwb, T, W, r, before);
     const long long acc_t = before * p.KVH;
     int t0, l2, h2;
     const int cnt = quad_row_tiles(p.start, p.nkeys, p.n, p.cap, r, t0, l2, h2);
     if (cnt > 0) {
       const long long Gs = acc_t + (long long)(head / p.G) * cnt;
-      ch = quad_wave_of(Gs + cnt - 1, T, W) - quad_wave_of(Gs, T, W) + 1;
+      ch = quad_wave_of(Gs + cnt - 1, T, W, p.qwa, p.qwb) - quad_wave_of(Gs, T, W, p.qwa, p.qwb) + 1;
     }
   } else if (hi > lo) {
     cl = lo / p.chunk;
@@ -1461,6 +1487,23 @@ static int quad_waves(int G, int qdt, int sdt) {
   return cache[dev][v];
 }
 
+// split weights of the quad pass 1's waves on even / odd XCDs: 21 : 19, i.e. 5% more tiles for an even-XCD wave.
+// Swept on two MI355X boxes at C2 (step µs, two runs each): 1:1 108.7 / 108.7, 41:39 108.4 / 108.2, 21:19 106.7 /
+// 107.2 and 106.9 / 106.9, 11:9 110.0, 23:17 111.5, 39:41 111.3.  LOCALS_AMD_DECODE_XW="a,b" overrides (1..1000).
+static void quad_weights(int& a, int& b) {
+  static const int packed = [] {  // thread-safe one-time initialisation
+    int x = 21, y = 19;
+    const char* e = getenv("LOCALS_AMD_DECODE_XW");
+    if (e && (sscanf(e, "%d,%d", &x, &y) != 2 || x < 1 || y < 1 || x > 1000 || y > 1000)) {
+      x = 21;
+      y = 19;
+    }
+    return (x << 16) | y;
+  }();
+  a = packed >> 16;
+  b = packed & 0xffff;
+}
+
 // the argument checks of lcl_qkv_attend (before anything touches the GPU)
 static int attend_args(const void* q, int qdt, const uint32_t* kw, const void* ks, const void* kb, const uint32_t* vw,
                        const void* vs, const void* vb, int sdt, int B, int H, int KVH, int hd, int cap, int n,
@@ -1560,6 +1603,7 @@ int lcl_qkv_attend_ex(const void* q, int qdt, const uint32_t* kw, const void* ks
     p.qmint = quad_mint(chunk);
     const long long tmax = (long long)B * KVH * ((n + kQT - 1) / kQT);
     p.qwaves = int(min((long long)quad_waves(p.G, qdt, sdt), max(1LL, tmax / p.qmint)));
+    quad_weights(p.qwa, p.qwb);
   }
   if (n > 0) {
     const dim3 grid = quad ? dim3(p.qwaves) : dim3(nparts, KVH * p.nslices, B);
@@ -1570,6 +1614,7 @@ int lcl_qkv_attend_ex(const void* q, int qdt, const uint32_t* kw, const void* ks
   c.pm = p.pm; c.pl = p.pl; c.po = p.po; c.sinks = sinks; c.out = out;
   c.start = start; c.nkeys = nullptr; c.n = n; c.cap = cap; c.H = H; c.nchunks = nparts; c.chunk = chunk; c.odt = qdt;
   c.quad = quad; c.R = B; c.KVH = KVH; c.G = p.G; c.qwaves = p.qwaves; c.qmint = p.qmint;
+  c.qwa = p.qwa; c.qwb = p.qwb;
   hipLaunchKernelGGL(decode_combine, dim3(B * H, comb_slices(B * H)), dim3(256), 0, stream, c);
   return int(hipGetLastError());
 }
