@@ -141,3 +141,52 @@ def test_snapshot_round_trip_decodes_identically(dev, tmp_path):
     qq = torch.cat([q, q])
     assert torch.equal(qkv.attend_cache(qq, m0, 0.0884, None, sinks).view(torch.int16),
                        qkv.attend_cache(qq, m1, 0.0884, None, sinks).view(torch.int16))
+
+
+@pytest.mark.parametrize("D", [128, 64])
+def test_move_rows_every_case(dev, D):
+    """qkv.move_rows (lcl_kv_gather) on its own, byte for byte against its definition: 40 destination rows (two
+    launches of 32 + 8), sources of different capacities, shifts below 0, 0 and above, lengths 0 / partial / whole,
+    rolls with every shift sign, a missing source, and a second kv-head layout (D = 64: 16 words, one scale)."""
+    from locals_amd import qkv
+
+    g = np.random.default_rng(77 + D)
+    KVH, cap = 3, 300
+
+    def rand_triple(B, c, seed):
+        t = _rand_triple(B, KVH, c, seed, dev)
+        if D == 64:
+            t = (t[0][..., :16].contiguous(), t[1][..., :1].contiguous(), t[2][..., :1].contiguous())
+        return t
+
+    srcs = [(rand_triple(4, c, 10 + i), rand_triple(4, c, 50 + i)) for i, c in enumerate((256, 300, 512))]
+    rows = []
+    for r in range(40):
+        si = int(g.integers(0, 3))
+        keys, values = srcs[si]
+        scap = keys[0].shape[2]
+        n = int(g.choice([0, 1, scap // 3, scap]))
+        shift = int(g.integers(-scap, cap))
+        wrap = bool(g.integers(0, 2))
+        if r == 7:
+            keys = values = None
+        rows.append((keys, values, int(g.integers(0, 4)), shift, n, wrap))
+    like = srcs[0]
+    got_k, got_v = qkv.move_rows(rows, cap, like)
+    torch.cuda.synchronize()
+    for which, got in ((0, got_k), (1, got_v)):
+        g_np = _np(got)
+        for a in range(3):
+            want = np.zeros_like(g_np[a])
+            for r, (keys, values, row, shift, n, wrap) in enumerate(rows):
+                src = keys if which == 0 else values
+                if src is None or n == 0:
+                    continue
+                s = _np(src)[a][row]  # (KVH, scap, per)
+                t = np.arange(cap) - shift
+                if wrap:
+                    want[r] = s[:, np.mod(t, n)]
+                else:
+                    ok = (t >= 0) & (t < n)
+                    want[r][:, ok] = s[:, t[ok]]
+            assert np.array_equal(g_np[a], want), (which, a)
