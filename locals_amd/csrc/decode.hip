@@ -81,7 +81,7 @@ struct DecodeParams {
   int kv_rows;  // rows of the KV buffers (B, or n_slots); a slot outside is clamped
   int R;        // query rows
   int qwaves, qmint;  // quad pass 1: waves launched, least tiles a wave
-  int qwa, qwb;       // quad pass 1: split weights of waves on even / odd XCDs
+  int qwa, qwb, qya, qyb, qold;  // quad pass 1: split weights (see quad_prefix)
   float scale_log2;
   const float* scale_dev;  // if set, the scale is read from device memory (times log2 e in the kernel)
   int qdt, sdt;
@@ -97,7 +97,7 @@ struct CombineParams {
   const int32_t* nkeys;
   int n, cap, H, nchunks, chunk, odt;
   int quad, R, KVH, G, qwaves, qmint;  // quad: parts are the stream-K slots of the quad pass 1
-  int qwa, qwb;
+  int qwa, qwb, qya, qyb, qold;
 };
 
 __device__ __forceinline__ void row_range(const int32_t* start, const int32_t* nkeys, int n, int cap, int r, int& lo,
@@ -484,24 +484,32 @@ __device__ __forceinline__ uint32_t row_take2(uint32_t x0, uint32_t x1) {
 // Stream-K split of the quad pass 1: the (row, kv head, 64-key tile) list in row-major order
 // (a row's tiles are the 64-aligned ones overlapping its keys [lo, hi)) is cut into W ranges,
 // W <= min(waves launched, total / mint), so every wave gets >= mint tiles and one resident
-// round of waves finishes together whatever the row lengths.  The ranges are weighted by the
-// XCD a wave runs on: one-wave workgroups go to XCD w mod 8 in turn, so even w run on even
-// XCDs (weight a) and odd w on odd ones (weight b); the odd XCDs' waves have run ~5% slower
-// on every MI355X measured.  A wave writes one partial for each (row, kv head) stream its
-// range touches, at slot j = wave - (wave holding the stream's first tile); pass 2
-// recomputes the same split.
-__device__ __forceinline__ long long quad_prefix(int w, int a, int b) {
-  return (long long)((w + 1) / 2) * a + (long long)(w / 2) * b;
+// round of waves finishes together whatever the row lengths.  The ranges are weighted by how
+// fast a wave runs, measured per wave on the MI355X (`s_memrealtime` at entry and exit):
+//  * by XCD: one-wave workgroups go to XCD w mod 8 in turn, so even w run on even XCDs and odd w
+//    on odd ones, and the odd XCDs' waves took ~10% longer a tile;
+//  * by age: the first `old` waves (one a SIMD) are each SIMD's older wave, which the SIMD's
+//    issue favours; the younger ones took ~22% longer a tile.
+// Weights: even old a, odd old b, even young c, odd young d (SplitW).  A wave writes one partial
+// for each (row, kv head) stream its range touches, at slot j = wave - (wave holding the
+// stream's first tile); pass 2 recomputes the same split.
+struct SplitW {
+  int a, b, c, d, old;  // old: even
+};
+__device__ __forceinline__ long long quad_prefix(int w, const SplitW& s) {
+  if (w <= s.old) return (long long)((w + 1) / 2) * s.a + (long long)(w / 2) * s.b;
+  const int y = w - s.old;
+  return (long long)(s.old / 2) * (s.a + s.b) + (long long)((y + 1) / 2) * s.c + (long long)(y / 2) * s.d;
 }
 // first global tile of wave w
-__device__ __forceinline__ long long quad_start(int w, long long T, int W, int a, int b) {
-  return T * quad_prefix(w, a, b) / quad_prefix(W, a, b);
+__device__ __forceinline__ long long quad_start(int w, long long T, int W, const SplitW& s) {
+  return T * quad_prefix(w, s) / quad_prefix(W, s);
 }
-// wave count: the lightest share keeps >= mint tiles (floor(T min(a, b) / Q) <= any range's length)
-__device__ __forceinline__ int quad_wave_count(long long T, int wlaunch, int mint, int a, int b) {
+// wave count: the lightest share keeps >= mint tiles (floor(T min weight / Q) <= any range's length)
+__device__ __forceinline__ int quad_wave_count(long long T, int wlaunch, int mint, const SplitW& s) {
   int W = int(min((long long)wlaunch, max(1LL, T / mint)));
-  const int m = min(a, b);
-  while (W > 1 && T * m < (long long)mint * quad_prefix(W, a, b)) W--;
+  const int m = min(min(s.a, s.b), min(s.c, s.d));
+  while (W > 1 && T * m < (long long)mint * quad_prefix(W, s)) W--;
   return W;
 }
 __device__ __forceinline__ int quad_row_tiles(const int32_t* start, const int32_t* nkeys, int n, int cap, int r,
@@ -535,7 +543,7 @@ __device__ __forceinline__ int wave_incl_scan(int x) {
 // total tiles T (all rows x KVH) and the wave count W of the split; with `row` >= 0 also the tiles of the rows
 // before it (`before`, in row units)
 __device__ __forceinline__ void quad_split(const int32_t* start, const int32_t* nkeys, int n, int cap, int R, int KVH,
-                                           int wlaunch, int mint, int a, int b, long long& T, int& W, int row,
+                                           int wlaunch, int mint, const SplitW& sw, long long& T, int& W, int row,
                                            long long& before) {
   const int lane = threadIdx.x & 63;
   long long t = 0;
@@ -547,7 +555,7 @@ __device__ __forceinline__ void quad_split(const int32_t* start, const int32_t* 
     t += __shfl(incl, 63);
   }
   T = t * KVH;
-  W = quad_wave_count(T, wlaunch, mint, a, b);
+  W = quad_wave_count(T, wlaunch, mint, sw);
 }
 
 // the row holding global tile g (0 <= g < T) and the global index of its first tile
@@ -583,11 +591,17 @@ __device__ __forceinline__ int quad_next_row(const int32_t* start, const int32_t
 }
 
 // wave holding global tile g (0 <= g < T): the largest w with quad_start(w) <= g, i.e. with
-// quad_prefix(w) <= X = floor(((g + 1) Q - 1) / T); the prefix grows by a, b, a, b, ...
-__device__ __forceinline__ int quad_wave_of(long long g, long long T, int W, int a, int b) {
-  const long long X = ((g + 1) * quad_prefix(W, a, b) - 1) / T;
-  const long long k = X / (a + b);
-  return int(2 * k + (X - k * (a + b) >= a ? 1 : 0));
+// quad_prefix(w) <= X = floor(((g + 1) Q - 1) / T); the prefix grows by a, b, a, b, ... up to
+// the old waves, then by c, d, c, d, ...
+__device__ __forceinline__ int quad_wave_of(long long g, long long T, int W, const SplitW& s) {
+  const long long X = ((g + 1) * quad_prefix(W, s) - 1) / T;
+  const long long Po = (long long)(s.old / 2) * (s.a + s.b);
+  if (X < Po || W <= s.old) {
+    const long long k = X / (s.a + s.b);
+    return int(2 * k + (X - k * (s.a + s.b) >= s.a ? 1 : 0));
+  }
+  const long long Y = X - Po, k = Y / (s.c + s.d);
+  return int(s.old + 2 * k + (Y - k * (s.c + s.d) >= s.c ? 1 : 0));
 }
 
 // a (row, kv head) stream of the quad pass 1
@@ -646,16 +660,17 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void
   constexpr int QB = QDT == DT_F32 ? 4 : 2;
 
   // ---- the split and this wave's first stream (one lane-parallel pass over the rows when R <= 64)
+  const SplitW sw{p.qwa, p.qwb, p.qya, p.qyb, p.qold};
   long long T, g, gend, row_first;
   int W, r0;
   if (p.R <= 64) {
     const int c = quad_lane_count(p.start, p.nkeys, p.n, p.cap, p.R, lane);
     const int incl = wave_incl_scan(c);
     T = uni((long long)__shfl(incl, 63) * p.KVH);
-    W = quad_wave_count(T, p.qwaves, p.qmint, p.qwa, p.qwb);
+    W = quad_wave_count(T, p.qwaves, p.qmint, sw);
     if (wv >= W) return;
-    g = quad_start(wv, T, W, p.qwa, p.qwb);
-    gend = quad_start(wv + 1, T, W, p.qwa, p.qwb);
+    g = quad_start(wv, T, W, sw);
+    gend = quad_start(wv + 1, T, W, sw);
     if (g >= gend) return;
     const long long lo_t = (long long)(incl - c) * p.KVH, hi_t = (long long)incl * p.KVH;
     const unsigned long long m = __ballot(c > 0 && g >= lo_t && g < hi_t);
@@ -663,12 +678,12 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void
     row_first = uni((long long)__shfl(incl - c, r0) * p.KVH);
   } else {
     long long unused;
-    quad_split(p.start, p.nkeys, p.n, p.cap, p.R, p.KVH, p.qwaves, p.qmint, p.qwa, p.qwb, T, W, -1, unused);
+    quad_split(p.start, p.nkeys, p.n, p.cap, p.R, p.KVH, p.qwaves, p.qmint, sw, T, W, -1, unused);
     T = uni(T);
     W = uni(W);
     if (wv >= W) return;
-    g = quad_start(wv, T, W, p.qwa, p.qwb);
-    gend = quad_start(wv + 1, T, W, p.qwa, p.qwb);
+    g = quad_start(wv, T, W, sw);
+    gend = quad_start(wv + 1, T, W, sw);
     if (g >= gend) return;
     r0 = uni(quad_locate(p.start, p.nkeys, p.n, p.cap, p.R, p.KVH, g, row_first));
     row_first = uni(row_first);
@@ -1046,7 +1061,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void
       wb1[e] += __shfl_xor(wb1[e], 16);
       wb1[e] += __shfl_xor(wb1[e], 32);
     }
-    const int jslot = wv - quad_wave_of(cur.Gs, T, W, p.qwa, p.qwb);
+    const int jslot = wv - quad_wave_of(cur.Gs, T, W, sw);
     // lanes of quad q4 < HG write head group q4: row i of O is head 4 q4 + i
     if (q4 < HG) {
       const int e = HG == 1 ? 0 : q4;
@@ -1297,13 +1312,14 @@ __global__ __launch_bounds__(256) void decode_combine(CombineParams p) {
   if (p.quad) {
     long long T, before;
     int W;
-    quad_split(p.start, p.nkeys, p.n, p.cap, p.R, p.KVH, p.qwaves, p.qmint, p.qwa, p.qwb, T, W, r, before);
+    const SplitW sw{p.qwa, p.qwb, p.qya, p.qyb, p.qold};
+    quad_split(p.start, p.nkeys, p.n, p.cap, p.R, p.KVH, p.qwaves, p.qmint, sw, T, W, r, before);
     const long long acc_t = before * p.KVH;
     int t0, l2, h2;
     const int cnt = quad_row_tiles(p.start, p.nkeys, p.n, p.cap, r, t0, l2, h2);
     if (cnt > 0) {
       const long long Gs = acc_t + (long long)(head / p.G) * cnt;
-      ch = quad_wave_of(Gs + cnt - 1, T, W, p.qwa, p.qwb) - quad_wave_of(Gs, T, W, p.qwa, p.qwb) + 1;
+      ch = quad_wave_of(Gs + cnt - 1, T, W, sw) - quad_wave_of(Gs, T, W, sw) + 1;
     }
   } else if (hi > lo) {
     cl = lo / p.chunk;
@@ -1487,21 +1503,38 @@ static int quad_waves(int G, int qdt, int sdt) {
   return cache[dev][v];
 }
 
-// split weights of the quad pass 1's waves on even / odd XCDs: 21 : 19, i.e. 5% more tiles for an even-XCD wave.
-// Swept on two MI355X boxes at C2 (step µs, two runs each): 1:1 108.7 / 108.7, 41:39 108.4 / 108.2, 21:19 106.7 /
-// 107.2 and 106.9 / 106.9, 11:9 110.0, 23:17 111.5, 39:41 111.3.  LOCALS_AMD_DECODE_XW="a,b" overrides (1..1000).
-static void quad_weights(int& a, int& b) {
-  static const int packed = [] {  // thread-safe one-time initialisation
-    int x = 21, y = 19;
+// Split weights of the quad pass 1 (see quad_prefix): even-XCD and odd-XCD waves among each SIMD's older waves,
+// then among its younger ones, in proportion to the tile rates measured per wave at C2 (4.12 / 4.55 / 5.06 /
+// 5.52 us a tile with equal weights).  The older waves are the first one a SIMD: 4 x the CU count.
+// LOCALS_AMD_DECODE_XW="a,b,c,d" overrides the weights (1..1000 each; "a,b" sets c = a, d = b).
+static void quad_weights(DecodeParams& p) {
+  static const long long packed = [] {  // thread-safe one-time initialisation
+    int w[4] = {24, 22, 20, 18};
     const char* e = getenv("LOCALS_AMD_DECODE_XW");
-    if (e && (sscanf(e, "%d,%d", &x, &y) != 2 || x < 1 || y < 1 || x > 1000 || y > 1000)) {
-      x = 21;
-      y = 19;
+    if (e) {
+      int x[4];
+      const int k = sscanf(e, "%d,%d,%d,%d", &x[0], &x[1], &x[2], &x[3]);
+      if (k == 2) x[2] = x[0], x[3] = x[1];
+      bool ok = k == 2 || k == 4;
+      for (int i = 0; ok && i < 4; i++) ok = x[i] >= 1 && x[i] <= 1000;
+      if (ok)
+        for (int i = 0; i < 4; i++) w[i] = x[i];
     }
-    return (x << 16) | y;
+    return ((long long)w[0] << 48) | ((long long)w[1] << 32) | ((long long)w[2] << 16) | (long long)w[3];
   }();
-  a = packed >> 16;
-  b = packed & 0xffff;
+  p.qwa = int((packed >> 48) & 0xffff);
+  p.qwb = int((packed >> 32) & 0xffff);
+  p.qya = int((packed >> 16) & 0xffff);
+  p.qyb = int(packed & 0xffff);
+  static int cus_of[64];  // CU count a device (0: not looked up yet; a racing lookup writes the same value)
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+  if (!cus_of[dev]) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
+    cus_of[dev] = cus;
+  }
+  p.qold = 4 * cus_of[dev];  // even (4 SIMDs a CU)
 }
 
 // the argument checks of lcl_qkv_attend (before anything touches the GPU)
@@ -1603,7 +1636,7 @@ int lcl_qkv_attend_ex(const void* q, int qdt, const uint32_t* kw, const void* ks
     p.qmint = quad_mint(chunk);
     const long long tmax = (long long)B * KVH * ((n + kQT - 1) / kQT);
     p.qwaves = int(min((long long)quad_waves(p.G, qdt, sdt), max(1LL, tmax / p.qmint)));
-    quad_weights(p.qwa, p.qwb);
+    quad_weights(p);
   }
   if (n > 0) {
     const dim3 grid = quad ? dim3(p.qwaves) : dim3(nparts, KVH * p.nslices, B);
@@ -1614,7 +1647,7 @@ int lcl_qkv_attend_ex(const void* q, int qdt, const uint32_t* kw, const void* ks
   c.pm = p.pm; c.pl = p.pl; c.po = p.po; c.sinks = sinks; c.out = out;
   c.start = start; c.nkeys = nullptr; c.n = n; c.cap = cap; c.H = H; c.nchunks = nparts; c.chunk = chunk; c.odt = qdt;
   c.quad = quad; c.R = B; c.KVH = KVH; c.G = p.G; c.qwaves = p.qwaves; c.qmint = p.qmint;
-  c.qwa = p.qwa; c.qwb = p.qwb;
+  c.qwa = p.qwa; c.qwb = p.qwb; c.qya = p.qya; c.qyb = p.qyb; c.qold = p.qold;
   hipLaunchKernelGGL(decode_combine, dim3(B * H, comb_slices(B * H)), dim3(256), 0, stream, c);
   return int(hipGetLastError());
 }
