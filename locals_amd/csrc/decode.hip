@@ -505,11 +505,13 @@ __device__ __forceinline__ long long quad_prefix(int w, const SplitW& s) {
 __device__ __forceinline__ long long quad_start(int w, long long T, int W, const SplitW& s) {
   return T * quad_prefix(w, s) / quad_prefix(W, s);
 }
-// wave count: the lightest share keeps >= mint tiles (floor(T min weight / Q) <= any range's length)
-__device__ __forceinline__ int quad_wave_count(long long T, int wlaunch, int mint, const SplitW& s) {
-  int W = int(min((long long)wlaunch, max(1LL, T / mint)));
+// wave count W = min(waves launched, T / mint); the weights stand only where the lightest share still gets >= mint
+// tiles (floor(T min weight / Q) <= any range's length), else every wave weighs the same (few tiles a wave: fewer
+// waves would cost more than uneven ones save).  Pass 1 and pass 2 take the same decision.
+__device__ __forceinline__ int quad_wave_count(long long T, int wlaunch, int mint, SplitW& s) {
+  const int W = int(min((long long)wlaunch, max(1LL, T / mint)));
   const int m = min(min(s.a, s.b), min(s.c, s.d));
-  while (W > 1 && T * m < (long long)mint * quad_prefix(W, s)) W--;
+  if (T * m < (long long)mint * quad_prefix(W, s)) s = SplitW{1, 1, 1, 1, s.old};
   return W;
 }
 __device__ __forceinline__ int quad_row_tiles(const int32_t* start, const int32_t* nkeys, int n, int cap, int r,
@@ -543,7 +545,7 @@ __device__ __forceinline__ int wave_incl_scan(int x) {
 // total tiles T (all rows x KVH) and the wave count W of the split; with `row` >= 0 also the tiles of the rows
 // before it (`before`, in row units)
 __device__ __forceinline__ void quad_split(const int32_t* start, const int32_t* nkeys, int n, int cap, int R, int KVH,
-                                           int wlaunch, int mint, const SplitW& sw, long long& T, int& W, int row,
+                                           int wlaunch, int mint, SplitW& sw, long long& T, int& W, int row,
                                            long long& before) {
   const int lane = threadIdx.x & 63;
   long long t = 0;
@@ -660,7 +662,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void
   constexpr int QB = QDT == DT_F32 ? 4 : 2;
 
   // ---- the split and this wave's first stream (one lane-parallel pass over the rows when R <= 64)
-  const SplitW sw{p.qwa, p.qwb, p.qya, p.qyb, p.qold};
+  SplitW sw{p.qwa, p.qwb, p.qya, p.qyb, p.qold};
   long long T, g, gend, row_first;
   int W, r0;
   if (p.R <= 64) {
@@ -1312,7 +1314,7 @@ __global__ __launch_bounds__(256) void decode_combine(CombineParams p) {
   if (p.quad) {
     long long T, before;
     int W;
-    const SplitW sw{p.qwa, p.qwb, p.qya, p.qyb, p.qold};
+    SplitW sw{p.qwa, p.qwb, p.qya, p.qyb, p.qold};
     quad_split(p.start, p.nkeys, p.n, p.cap, p.R, p.KVH, p.qwaves, p.qmint, sw, T, W, r, before);
     const long long acc_t = before * p.KVH;
     int t0, l2, h2;
