@@ -567,7 +567,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   } else {
     // 16-bit: wave w loads key rows 16 w .. 16 w + 15 of K and of V (4 instructions of 1 KB each), chunk c of
     // row r to slot c ^ swk(r) (K) or c ^ swv(r) (V)
-    constexpr int kWaitOne = (0xF << 8) | (0x7 << 4) | 8;  // vmcnt(8): the other slot's loads may stay in flight
     constexpr int kWaitAll = (0xF << 8) | (0x7 << 4);
     constexpr int kWaitLds = (0x3 << 14) | (0x7 << 4) | 0xF;
     auto barrier = [&]() __attribute__((always_inline)) {
@@ -596,26 +595,26 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         for (int i = 0; i < 4; i++) row[i] = krow[i] = make_uint4(0u, 0u, 0u, 0u);
       }
     };
-    auto step = [&](int t0, uint8_t* S) __attribute__((always_inline)) {
-      if (t0 + kKT < khi) __builtin_amdgcn_s_waitcnt(kWaitOne);
-      else __builtin_amdgcn_s_waitcnt(kWaitAll);
-      barrier();  // every wave's loads of this tile are in the slot
+    // One barrier a tile: at its top every wave's loads of this tile are in slot S and every wave is done with
+    // the previous tile, whose slot (Snext) then takes the next tile's loads, in flight while this tile is
+    // multiplied.
+    auto step = [&](int t0, uint8_t* S, uint8_t* Snext) __attribute__((always_inline)) {
+      __builtin_amdgcn_s_waitcnt(kWaitAll);  // this wave's loads of the tile: the only ones in flight
+      barrier();
+      if (t0 + kKT < khi) dma16t(t0 + kKT, Snext);
       if (t0 < klo || t0 + kKT > khi) {
         clear_v(t0, S);
         barrier();
       }
       compute(t0, S);
-      barrier();  // every wave is done with the slot
-      if (t0 + 2 * kKT < khi) dma16t(t0 + 2 * kKT, S);
     };
     dma16t(tfirst, raw0);
-    if (tfirst + kKT < khi) dma16t(tfirst + kKT, raw1);
     load_q();
     for (int t0 = tfirst;;) {
-      step(t0, raw0);
+      step(t0, raw0, raw1);
       t0 += kKT;
       if (t0 >= khi) break;
-      step(t0, raw1);
+      step(t0, raw1, raw0);
       t0 += kKT;
       if (t0 >= khi) break;
     }
