@@ -142,11 +142,69 @@ __global__ __launch_bounds__(256) void dequantize_pair_p2(DequantPair pp) {
   dequantize_p2_block<WSH>(blockIdx.y ? pp.d[1] : pp.d[0]);
 }
 
+// The same pass with 16-byte accesses for 16-bit output and 16-byte aligned buffers: 8 words (32 codes) a thread,
+// two 16-byte loads 1 KB apart in its wave's 2 KB run, both issued before either is used (codes streamed from
+// HBM keep two requests a lane in flight instead of one), then four 16-byte stores.  The same arithmetic as
+// dequantize_rows: one fp32 fused multiply-add a value, rounded once to the output type.
+template <int ODT>
+__global__ __launch_bounds__(256) void dequantize_pair_x16(DequantPair pp) {
+  const DequantParams& p = blockIdx.y ? pp.d[1] : pp.d[0];
+  const long long nw = p.rows * 32;  // rows of 128 values: 32 words each
+  const long long w0 = static_cast<long long>(blockIdx.x) * 2048 + (threadIdx.x >> 6) * 512 + 4 * (threadIdx.x & 63);
+  u4 x[2];
+  float s[2], b[2];
+#pragma unroll
+  for (int h = 0; h < 2; h++) {
+    const long long wid = w0 + 256 * h;
+    const bool in = wid < nw;  // nw and wid are multiples of 4: a lane's 4 words are all in or all out
+    x[h] = in ? __builtin_nontemporal_load(reinterpret_cast<const u4*>(p.words + wid)) : u4{0u, 0u, 0u, 0u};
+    s[h] = in ? load_as_f32(p.scales, size_t(wid >> 4), p.sdt) : 0.0f;
+    b[h] = in ? load_as_f32(p.biases, size_t(wid >> 4), p.sdt) : 0.0f;
+  }
+#pragma unroll
+  for (int h = 0; h < 2; h++) {
+    const long long wid = w0 + 256 * h;
+    if (wid >= nw) continue;
+    uint32_t o[8];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const uint32_t w = x[h][j];
+      float v[4];
+#pragma unroll
+      for (int i = 0; i < 4; i++) v[i] = s[h] * float((w >> (8 * i)) & 0xffu) + b[h];
+      if constexpr (ODT == DT_BF16) {
+        o[2 * j] = f32_to_bf16_bits(v[0]) | (uint32_t(f32_to_bf16_bits(v[1])) << 16);
+        o[2 * j + 1] = f32_to_bf16_bits(v[2]) | (uint32_t(f32_to_bf16_bits(v[3])) << 16);
+      } else {
+        o[2 * j] = __builtin_bit_cast(uint16_t, _Float16(v[0])) |
+                   (uint32_t(__builtin_bit_cast(uint16_t, _Float16(v[1]))) << 16);
+        o[2 * j + 1] = __builtin_bit_cast(uint16_t, _Float16(v[2])) |
+                       (uint32_t(__builtin_bit_cast(uint16_t, _Float16(v[3]))) << 16);
+      }
+    }
+    u4* dst = reinterpret_cast<u4*>(static_cast<uint16_t*>(p.out) + wid * 4);
+    dst[0] = u4{o[0], o[1], o[2], o[3]};
+    dst[1] = u4{o[4], o[5], o[6], o[7]};
+  }
+}
+
 // K and V (rows of 128 values each) of an 8-bit cache dequantized to 16 bits in one launch.  Declared in
 // lcl_common.h for the masked-attention entry point; 0 or a hipError_t.
 int dequantize_kv128(const uint32_t* kw, const void* ks, const void* kb, const uint32_t* vw, const void* vs,
                      const void* vb, int sdt, long long rows, void* kout, void* vout, hipStream_t stream) {
   DequantPair pp{{{kw, ks, kb, kout, rows, 128, sdt, sdt}, {vw, vs, vb, vout, rows, 128, sdt, sdt}}};
+  const auto a16 = [](const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15u) == 0; };
+  if (a16(kw) && a16(vw) && a16(kout) && a16(vout) && (sdt == DT_F16 || sdt == DT_BF16)) {
+    const long long blocks = (rows * 32 + 2047) / 2048;
+    if (blocks > 0x7fffffffLL) return int(hipErrorInvalidValue);
+    if (sdt == DT_BF16)
+      hipLaunchKernelGGL(dequantize_pair_x16<DT_BF16>, dim3(static_cast<unsigned>(blocks), 2), dim3(256), 0, stream,
+                         pp);
+    else
+      hipLaunchKernelGGL(dequantize_pair_x16<DT_F16>, dim3(static_cast<unsigned>(blocks), 2), dim3(256), 0, stream,
+                         pp);
+    return int(hipGetLastError());
+  }
   const long long blocks = (rows * 32 + 1023) / 1024;
   if (blocks > 0x7fffffffLL) return int(hipErrorInvalidValue);
   hipLaunchKernelGGL(dequantize_pair_p2<5>, dim3(static_cast<unsigned>(blocks), 2), dim3(256), 0, stream, pp);
