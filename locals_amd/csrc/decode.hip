@@ -505,13 +505,20 @@ __device__ __forceinline__ long long quad_prefix(int w, const SplitW& s) {
 __device__ __forceinline__ long long quad_start(int w, long long T, int W, const SplitW& s) {
   return T * quad_prefix(w, s) / quad_prefix(W, s);
 }
-// wave count W = min(waves launched, T / mint); the weights stand only where the lightest share still gets >= mint
-// tiles (floor(T min weight / Q) <= any range's length), else every wave weighs the same (few tiles a wave: fewer
-// waves would cost more than uneven ones save).  Pass 1 and pass 2 take the same decision.
+// whether every share of W waves under weights s keeps >= mint tiles (floor(T min weight / Q) <= any range's length)
+__device__ __forceinline__ bool quad_split_ok(long long T, int W, int mint, const SplitW& s) {
+  const int m = min(min(s.a, s.b), min(s.c, s.d));
+  return T * m >= (long long)mint * quad_prefix(W, s);
+}
+// wave count W = min(waves launched, T / mint).  The weights stand where the lightest share still gets >= mint tiles;
+// else the milder 24 : 22 : 20 : 18, if that fits; else every wave weighs the same (few tiles a wave: fewer waves
+// would cost more than uneven ones save).  Pass 1 and pass 2 take the same decision.
 __device__ __forceinline__ int quad_wave_count(long long T, int wlaunch, int mint, SplitW& s) {
   const int W = int(min((long long)wlaunch, max(1LL, T / mint)));
-  const int m = min(min(s.a, s.b), min(s.c, s.d));
-  if (T * m < (long long)mint * quad_prefix(W, s)) s = SplitW{1, 1, 1, 1, s.old};
+  if (!quad_split_ok(T, W, mint, s)) {
+    const SplitW mild{24, 22, 20, 18, s.old};
+    s = quad_split_ok(T, W, mint, mild) ? mild : SplitW{1, 1, 1, 1, s.old};
+  }
   return W;
 }
 __device__ __forceinline__ int quad_row_tiles(const int32_t* start, const int32_t* nkeys, int n, int cap, int r,
@@ -1506,12 +1513,14 @@ static int quad_waves(int G, int qdt, int sdt) {
 }
 
 // Split weights of the quad pass 1 (see quad_prefix): even-XCD and odd-XCD waves among each SIMD's older waves,
-// then among its younger ones, in proportion to the tile rates measured per wave at C2 (4.12 / 4.55 / 5.06 /
-// 5.52 us a tile with equal weights).  The older waves are the first one a SIMD: 4 x the CU count.
+// then among its younger ones.  The tile rates measured per wave at C2 on one MI355X (4.12 / 4.55 / 5.06 / 5.52 us
+// a tile with equal weights) give 24 : 22 : 20 : 18; on slower parts the odd XCDs lag more, and 26 : 22 : 20 : 16
+// ran C2 1-1.5 us faster there (quad_wave_count falls back to 24 : 22 : 20 : 18 where a share would get too few
+// tiles).  The older waves are the first one a SIMD: 4 x the CU count.
 // LOCALS_AMD_DECODE_XW="a,b,c,d" overrides the weights (1..1000 each; "a,b" sets c = a, d = b).
 static void quad_weights(DecodeParams& p) {
   static const long long packed = [] {  // thread-safe one-time initialisation
-    int w[4] = {24, 22, 20, 18};
+    int w[4] = {26, 22, 20, 16};
     const char* e = getenv("LOCALS_AMD_DECODE_XW");
     if (e) {
       int x[4];
