@@ -644,7 +644,9 @@ struct QRsrc {
 };
 __device__ __forceinline__ QRsrc quad_rsrc(const DecodeParams& p, const QStream& S) {
   const int slot = p.slots ? min(max(p.slots[S.r], 0), p.kv_rows - 1) : S.r;
-  const size_t tok0 = (size_t(slot) * p.KVH + S.kvh) * p.cap;
+  // the slot comes through a vector load, so the offset is marked uniform here: a descriptor base the compiler
+  // takes for divergent puts a readfirstlane loop around every load through it
+  const size_t tok0 = size_t(uni((long long)((size_t(slot) * p.KVH + S.kvh) * p.cap)));
   const uint32_t cap = uint32_t(p.cap);
   QRsrc d;
   d.rk = make_rsrc(p.kw + tok0 * 32, cap * 128u);
@@ -658,8 +660,8 @@ __device__ __forceinline__ QRsrc quad_rsrc(const DecodeParams& p, const QStream&
 // the G query rows of a stream (rows past G read as 0)
 template <int QB>
 __device__ __forceinline__ BufRsrc quad_qrsrc(const DecodeParams& p, const QStream& S) {
-  return make_rsrc(static_cast<const uint8_t*>(p.q) + (size_t(S.r) * p.H + size_t(S.kvh) * p.G) * kHD * QB,
-                   uint32_t(p.G * kHD * QB));
+  const size_t off = size_t(uni((long long)((size_t(S.r) * p.H + size_t(S.kvh) * p.G) * kHD * QB)));
+  return make_rsrc(static_cast<const uint8_t*>(p.q) + off, uint32_t(p.G * kHD * QB));
 }
 
 template <int QDT, int SDT, int HG>
@@ -678,8 +680,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void
     T = uni((long long)__shfl(incl, 63) * p.KVH);
     W = quad_wave_count(T, p.qwaves, p.qmint, sw);
     if (wv >= W) return;
-    g = quad_start(wv, T, W, sw);
-    gend = quad_start(wv + 1, T, W, sw);
+    g = uni(quad_start(wv, T, W, sw));
+    gend = uni(quad_start(wv + 1, T, W, sw));
     if (g >= gend) return;
     const long long lo_t = (long long)(incl - c) * p.KVH, hi_t = (long long)incl * p.KVH;
     const unsigned long long m = __ballot(c > 0 && g >= lo_t && g < hi_t);
@@ -691,8 +693,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void
     T = uni(T);
     W = uni(W);
     if (wv >= W) return;
-    g = quad_start(wv, T, W, sw);
-    gend = quad_start(wv + 1, T, W, sw);
+    g = uni(quad_start(wv, T, W, sw));
+    gend = uni(quad_start(wv + 1, T, W, sw));
     if (g >= gend) return;
     r0 = uni(quad_locate(p.start, p.nkeys, p.n, p.cap, p.R, p.KVH, g, row_first));
     row_first = uni(row_first);
@@ -759,14 +761,14 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void
   cur.kvh = int((g - row_first) / cur.cnt);
   cur.Gs = row_first + (long long)cur.kvh * cur.cnt;
   cur = uni(cur);
-  int k0 = int(g - cur.Gs);
+  int k0 = uni(int(g - cur.Gs));
   issue(quad_rsrc(p, cur), cur, k0);
   issue_q(cur);
 
   for (;;) {
     // the segment: tiles [k0, k1) of stream cur; its first tile and q are in flight
     const long long seg_end = min(gend, cur.Gs + cur.cnt);
-    const int k1 = int(seg_end - cur.Gs);
+    const int k1 = uni(int(seg_end - cur.Gs));
     const bool more = seg_end < gend;
     QStream nxt = cur;  // the next stream (the next kv head, or the next row with keys), when there is one
     if (more) {
