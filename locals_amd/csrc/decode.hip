@@ -507,12 +507,13 @@ __device__ __forceinline__ long long quad_start(int w, long long T, int W, const
 }
 // whether every share of W waves under weights s keeps >= mint tiles (floor(T min weight / Q) <= any range's length)
 __device__ __forceinline__ bool quad_split_ok(long long T, int W, int mint, const SplitW& s) {
-  const int m = min(min(s.a, s.b), min(s.c, s.d));
+  const int m = W <= s.old ? min(s.a, s.b) : min(min(s.a, s.b), min(s.c, s.d));  // the weights in use
   return T * m >= (long long)mint * quad_prefix(W, s);
 }
 // wave count W = min(waves launched, T / mint).  The weights stand where the lightest share still gets >= mint tiles;
-// else the milder 24 : 22 : 20 : 18, if that fits; else every wave weighs the same (few tiles a wave: fewer waves
-// would cost more than uneven ones save).  Pass 1 and pass 2 take the same decision.
+// else the default 24 : 22 : 20 : 18 (for stronger weights set through LOCALS_AMD_DECODE_XW), if that fits; else every
+// wave weighs the same (few tiles a wave: fewer waves would cost more than uneven ones save).  Pass 1 and pass 2 take
+// the same decision.
 __device__ __forceinline__ int quad_wave_count(long long T, int wlaunch, int mint, SplitW& s) {
   const int W = int(min((long long)wlaunch, max(1LL, T / mint)));
   if (!quad_split_ok(T, W, mint, s)) {
@@ -1496,8 +1497,11 @@ static int quad_hg2_per_cu(int qdt, int sdt) {
                                                                            : quad_hg2_per_cu<DT_F32, DT_F16>();
 }
 
-// waves of the quad pass 1, one resident round: two a SIMD for G <= 4 (the kernel's occupancy), the occupancy
-// calculator's count for 5 <= G <= 8
+// waves of the quad pass 1, one resident round: one a SIMD for G <= 4 (the kernel's occupancy allows two, but at one
+// a SIMD each wave issues alone and pass 2 joins half the parts: C2 105.3-105.5 us a step against 107.5-107.8 at
+// two, C3 91.8-92.6 against 95.3-95.6, C4's decode rows 60.7-61.0 against 63.8-64.1; counts between the two, such
+// as 1152 or 1408 waves on 256 CUs, ran slower than either), the occupancy calculator's count for 5 <= G <= 8
+// (Flint's G = 8: 68 us at 1792 waves, 72.5 at 1024)
 static int quad_waves(int G, int qdt, int sdt) {
   static int cache[64][7] = {{0}};  // [device][0: G <= 4, 1 + 2 qdt + sdt: the two-group kernel]
   int dev = 0;
@@ -1506,7 +1510,7 @@ static int quad_waves(int G, int qdt, int sdt) {
   if (!cache[dev][v]) {
     int cus = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
-    cache[dev][v] = (v == 0 ? 2 * 4 : quad_hg2_per_cu(qdt, sdt)) * cus;
+    cache[dev][v] = (v == 0 ? 4 : quad_hg2_per_cu(qdt, sdt)) * cus;
     // LOCALS_AMD_DECODE_WAVES overrides the count (a tuning knob: fewer waves than resident slots)
     const char* e = getenv("LOCALS_AMD_DECODE_WAVES");
     if (e && atoi(e) > 0) cache[dev][v] = atoi(e);
@@ -1516,13 +1520,13 @@ static int quad_waves(int G, int qdt, int sdt) {
 
 // Split weights of the quad pass 1 (see quad_prefix): even-XCD and odd-XCD waves among each SIMD's older waves,
 // then among its younger ones.  The tile rates measured per wave at C2 on one MI355X (4.12 / 4.55 / 5.06 / 5.52 us
-// a tile with equal weights) give 24 : 22 : 20 : 18; on slower parts the odd XCDs lag more, and 26 : 22 : 20 : 16
-// ran C2 1-1.5 us faster there (quad_wave_count falls back to 24 : 22 : 20 : 18 where a share would get too few
-// tiles).  The older waves are the first one a SIMD: 4 x the CU count.
+// a tile with equal weights, two waves a SIMD) give 24 : 22 : 20 : 18.  With one wave a SIMD (G <= 4) only the
+// first pair applies; 24 : 22 ran C2, C3 and C4's decode rows fastest there (against 22 : 22 up to 30 : 22).  The
+// older waves are the first one a SIMD: 4 x the CU count.
 // LOCALS_AMD_DECODE_XW="a,b,c,d" overrides the weights (1..1000 each; "a,b" sets c = a, d = b).
 static void quad_weights(DecodeParams& p) {
   static const long long packed = [] {  // thread-safe one-time initialisation
-    int w[4] = {26, 22, 20, 16};
+    int w[4] = {24, 22, 20, 18};
     const char* e = getenv("LOCALS_AMD_DECODE_XW");
     if (e) {
       int x[4];
