@@ -674,19 +674,33 @@ __global__ __launch_bounds__(256) void sdpa_combine(SdpaCombineParams p) {
   const float4* po4 = reinterpret_cast<const float4*>(p.po) + base * (kD / 4) + lane;
   float m = -INFINITY, L = 0.0f;
   float4 o = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-#pragma unroll 8
-  for (int c = 0; c < p.nchunks; c++) {
-    const float mc = p.pm[base + c], lc = p.pl[base + c];
-    const float4 oc = po4[size_t(c) * (kD / 4)];
-    if (!(mc > -INFINITY)) continue;
-    const float mn = fmaxf(m, mc);
-    const float a = m == -INFINITY ? 0.0f : fast_exp2(m - mn), w = fast_exp2(mc - mn);
-    o.x = o.x * a + oc.x * w;
-    o.y = o.y * a + oc.y * w;
-    o.z = o.z * a + oc.z * w;
-    o.w = o.w * a + oc.w * w;
-    L = L * a + lc * w;
-    m = mn;
+  // eight chunks at a time, all their loads issued before any merge: the index is clamped rather than tested, so
+  // the loads sit in one block (a test around each made every chunk a load-wait-load-wait round trip), and a chunk
+  // with no key (m = -inf, its o left unwritten) is merged by selects as weight 0 -- the same result as skipping it
+  for (int c0 = 0; c0 < p.nchunks; c0 += 8) {
+    float mc[8], lc[8];
+    float4 oc[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const int c = min(c0 + i, p.nchunks - 1);
+      mc[i] = p.pm[base + c];
+      lc[i] = p.pl[base + c];
+      oc[i] = po4[size_t(c) * (kD / 4)];
+    }
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const bool ok = c0 + i < p.nchunks && mc[i] > -INFINITY;
+      const float mn = ok ? fmaxf(m, mc[i]) : m;
+      const float a = !ok ? 1.0f : m == -INFINITY ? 0.0f : fast_exp2(m - mn), w = ok ? fast_exp2(mc[i] - mn) : 0.0f;
+      const float4 x = ok ? oc[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      const float lx = ok ? lc[i] : 0.0f;
+      o.x = o.x * a + x.x * w;
+      o.y = o.y * a + x.y * w;
+      o.z = o.z * a + x.z * w;
+      o.w = o.w * a + x.w * w;
+      L = L * a + lx * w;
+      m = mn;
+    }
   }
   const float sink = p.sinks ? p.sinks[head] * kLog2e : -INFINITY;
   const float M = fmaxf(m, sink);
