@@ -151,8 +151,9 @@ __device__ __forceinline__ uint2 lds_read_tr16(const uint8_t* p) {
 }
 
 // One workgroup: RT x 64 rows of (batch row b, kv head kvh) -- a row is one (query, head) -- and the keys of
-// chunk c.  8-bit: per 64-key tile the raw bytes arrive in one of two LDS slots while the other's tile is
-// dequantized into the operand buffer and multiplied.  16-bit: the K and V tiles arrive in one of two slots and
+// chunk c.  8-bit, two row tiles: per 64-key tile the raw bytes arrive in one of two LDS slots while the other's
+// tile is dequantized into the operand buffer and multiplied; one row tile: the codes arrive in registers two tiles
+// ahead and are dequantized into one of two operand buffers while the other's tile is multiplied.  16-bit: the K and V tiles arrive in one of two slots and
 // are multiplied in place while the next tile's loads are in flight.
 template <int QDT, int SDT, int FMT, int MT, int MASK, int RT>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void sdpa_pass1(SdpaParams p) {
@@ -214,10 +215,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   // transposing read).  16-bit: the K and V tiles arrive the same way
   // (chunks swizzled by swk / swv) and are the MFMA operands themselves -- K rows read as they are, V^T through the
   // transposing read -- so nothing is staged.
-  __shared__ __attribute__((aligned(16))) uint16_t Ks[FMT == KV_Q8 ? kKT * kKsStride : 8];
-  __shared__ __attribute__((aligned(16))) uint8_t Vk[FMT == KV_Q8 ? kKT * 256 : 16];
-  __shared__ __attribute__((aligned(16))) uint8_t raw0[FMT == KV_Q8 ? kRawSlot : kRaw16];
-  __shared__ __attribute__((aligned(16))) uint8_t raw1[FMT == KV_Q8 ? kRawSlot : kRaw16];
+  // 8-bit with one row tile: the codes come into registers two tiles ahead and there are two operand buffers
+  // (tile i multiplied from buffer i % 2 while tile i + 1 is staged into the other: one barrier a tile); the raw
+  // slots are then unused
+  constexpr bool kRegPipe = FMT == KV_Q8 && RT == 1;
+  constexpr int kOpBufs = kRegPipe ? 2 : 1;
+  __shared__ __attribute__((aligned(16))) uint16_t Ks[FMT == KV_Q8 ? kOpBufs * kKT * kKsStride : 8];
+  __shared__ __attribute__((aligned(16))) uint8_t Vk[FMT == KV_Q8 ? kOpBufs * kKT * 256 : 16];
+  __shared__ __attribute__((aligned(16))) uint8_t raw0[kRegPipe ? 16 : FMT == KV_Q8 ? kRawSlot : kRaw16];
+  __shared__ __attribute__((aligned(16))) uint8_t raw1[kRegPipe ? 16 : FMT == KV_Q8 ? kRawSlot : kRaw16];
 
   // Q^T as B operands: qb[r][kk] = scale log2(e) q[row][32 kk + 8 q4 + j], scaled in fp32 before its one rounding
   // to the MFMA type, so the products come out as base-2 logits.  Loaded (16 bytes a lane a step) after the first
@@ -299,6 +305,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     T.vs = *reinterpret_cast<const uint32_t*>(S + 16896 + 4 * kkey);
     T.vb = *reinterpret_cast<const uint32_t*>(S + 17152 + 4 * kkey);
   };
+  // the same share loaded from the buffers into registers (register pipeline)
+  auto load_glb = [&](int t0, RawTile& T) __attribute__((always_inline)) {
+    const uint32_t key = uint32_t(t0 + kkey), co = key * 128u + 32u * uint32_t(kpart);
+    T.k[0] = buf_load_b128(rk, co, 0);
+    T.k[1] = buf_load_b128(rk, co, 16);
+    T.v[0] = buf_load_b128(rv, co, 0);
+    T.v[1] = buf_load_b128(rv, co, 16);
+    T.ks = buf_load_b32(rks, key * 4u, 0);
+    T.kb = buf_load_b32(rkb, key * 4u, 0);
+    T.vs = buf_load_b32(rvs, key * 4u, 0);
+    T.vb = buf_load_b32(rvb, key * 4u, 0);
+  };
 
   // dequantize 32 codes (dims 32 kpart ..) with the key's scale / bias pair: 16 packed pairs of the MFMA type
   auto dequant = [&](const u4 (&c)[2], uint32_t sc, uint32_t bi, uint32_t (&o)[16]) __attribute__((always_inline)) {
@@ -324,13 +342,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   // dequantize an 8-bit tile into the operand buffers: K rows into Ks, V rows into Vk (16-byte chunk c of key r at
   // slot c ^ swv(r)); keys outside [klo, khi) become 0 (MASKED: the tile straddles an end of the range;
   // otherwise every key is inside and no test is made)
-  auto stage = [&](int t0, const RawTile& T, auto masked) __attribute__((always_inline)) {
+  auto stage = [&](int t0, const RawTile& T, auto masked, int ob) __attribute__((always_inline)) {
     constexpr bool MASKED = decltype(masked)::value;
     const int kg = t0 + kkey;
     const bool kin = !MASKED || (kg >= klo && kg < khi);
     uint32_t o[16];
     dequant(T.k, T.ks, T.kb, o);
-    uint4* kdst = reinterpret_cast<uint4*>(&Ks[kkey * kKsStride + kpart * 32]);
+    uint4* kdst = reinterpret_cast<uint4*>(&Ks[ob * (kKT * kKsStride) + kkey * kKsStride + kpart * 32]);
 #pragma unroll
     for (int u = 0; u < 4; u++)
       kdst[u] = kin ? make_uint4(o[4 * u], o[4 * u + 1], o[4 * u + 2], o[4 * u + 3]) : make_uint4(0u, 0u, 0u, 0u);
@@ -338,7 +356,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const int sw = swv(kkey);
 #pragma unroll
     for (int u = 0; u < 4; u++)
-      *reinterpret_cast<uint4*>(&Vk[kkey * 256 + 16 * ((4 * kpart + u) ^ sw)]) =
+      *reinterpret_cast<uint4*>(&Vk[ob * (kKT * 256) + kkey * 256 + 16 * ((4 * kpart + u) ^ sw)]) =
           kin ? make_uint4(o[4 * u], o[4 * u + 1], o[4 * u + 2], o[4 * u + 3]) : make_uint4(0u, 0u, 0u, 0u);
   };
 
@@ -380,15 +398,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const int sk16 = swk(c16);
   const int vkey16 = 4 * q4 + (c16 >> 2), vsw16 = swv(vkey16);
   const int vch16 = (c16 & 3) >> 1, voff16 = vkey16 * 256 + 8 * (c16 & 1);
-  auto kfrag = [&](const uint8_t* S, int t, int kk) __attribute__((always_inline)) -> uint4 {
+  auto kfrag = [&](const uint8_t* S, int ob, int t, int kk) __attribute__((always_inline)) -> uint4 {
     if constexpr (FMT == KV_Q8)
-      return *reinterpret_cast<const uint4*>(&Ks[(16 * t + c16) * kKsStride + 8 * q4 + 32 * kk]);
+      return *reinterpret_cast<const uint4*>(&Ks[ob * (kKT * kKsStride) + (16 * t + c16) * kKsStride + 8 * q4 + 32 * kk]);
     else
       return *reinterpret_cast<const uint4*>(S + (16 * t + c16) * 256 + 16 * ((4 * kk + q4) ^ sk16));
   };
-  auto vfrag = [&](const uint8_t* S, int u, int dd) __attribute__((always_inline)) -> uint4 {
+  auto vfrag = [&](const uint8_t* S, int ob, int u, int dd) __attribute__((always_inline)) -> uint4 {
     // the V region: the slot's second half (16-bit), the dequantized buffer Vk (8-bit), the same layout
-    const uint8_t* a = (FMT == KV_Q8 ? Vk : S + 16384) + voff16 + 32 * u * 256 + 16 * ((2 * dd + vch16) ^ vsw16);
+    const uint8_t* a =
+        (FMT == KV_Q8 ? Vk + ob * (kKT * 256) : S + 16384) + voff16 + 32 * u * 256 + 16 * ((2 * dd + vch16) ^ vsw16);
     const uint2 lo = lds_read_tr16(a), hi = lds_read_tr16(a + 16 * 256);
     return make_uint4(lo.x, lo.y, hi.x, hi.y);
   };
@@ -410,7 +429,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     if constexpr (MASK == MK_DENSE) ok = ok & (drow[r][min(max(j, 0), p.N - 1) * p.msk] != 0);
     return ok;
   };
-  auto compute = [&](int t0, const uint8_t* S) __attribute__((always_inline)) {
+  auto compute = [&](int t0, const uint8_t* S, int ob) __attribute__((always_inline)) {
     // S^T = K Q^T: st[r][t][i] = S[row][t0 + 16 t + 4 q4 + i].  Where registers allow (causal mask, one row
     // tile), the 32-dim step kk is the outer loop, so the 4 RT accumulators are independent chains and a step's
     // four K fragments are read together; otherwise a key block t at a time.
@@ -431,7 +450,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       // outside [klo, khi) were cleared in the slot (16-bit) or dequantized as 0 (8-bit).
       uint4 kf[4];
 #pragma unroll
-      for (int t = 0; t < 4; t++) kf[t] = kfrag(S, t, 0);
+      for (int t = 0; t < 4; t++) kf[t] = kfrag(S, ob, t, 0);
       if (full) {
 #pragma unroll
         for (int t = 0; t < 4; t++)
@@ -453,7 +472,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
       for (int kk = 1; kk < 4; kk++) {
 #pragma unroll
-        for (int t = 0; t < 4; t++) kf[t] = kfrag(S, t, kk);
+        for (int t = 0; t < 4; t++) kf[t] = kfrag(S, ob, t, kk);
 #pragma unroll
         for (int t = 0; t < 4; t++)
 #pragma unroll
@@ -464,7 +483,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       for (int t = 0; t < 4; t++)
 #pragma unroll
         for (int kk = 0; kk < 4; kk++) {
-          const uint4 kf = kfrag(S, t, kk);
+          const uint4 kf = kfrag(S, ob, t, kk);
 #pragma unroll
           for (int r = 0; r < RT; r++) st[r][t] = mma32<MT>(kf, qb[r][kk], kk ? st[r][t] : negm[r]);
         }
@@ -520,7 +539,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     for (int u = 0; u < 2; u++) {
 #pragma unroll
       for (int dd = 0; dd < 8; dd++) {
-        const uint4 vf = vfrag(S, u, dd);
+        const uint4 vf = vfrag(S, ob, u, dd);
 #pragma unroll
         for (int r = 0; r < RT; r++) O[r][dd] = mma32<MT>(vf, pb[r][u], O[r][dd]);
       }
@@ -530,7 +549,44 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   };
 
   const int tfirst = klo & ~(kKT - 1);
-  if constexpr (FMT == KV_Q8) {
+  if constexpr (kRegPipe) {
+    constexpr int kWaitLds = (0x3 << 14) | (0x7 << 4) | 0xF;
+    auto barrier = [&]() __attribute__((always_inline)) {
+      __builtin_amdgcn_s_waitcnt(kWaitLds);
+      __builtin_amdgcn_s_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+    };
+    auto stage_any = [&](int t0, const RawTile& T, int ob) __attribute__((always_inline)) {
+      if (t0 >= klo && t0 + kKT <= khi) stage(t0, T, std::false_type{}, ob);
+      else stage(t0, T, std::true_type{}, ob);
+    };
+    // tile i's codes sit in TA (i even) or TB (i odd) from two steps before it is staged.  Every step issues its
+    // loads, past the last tile as a reload of it (an L2 hit): with a load skipped on some path, the in-order
+    // counter could no longer wait for one tile's loads while the next tile's stay in flight.
+    const int tlast = (khi - 1) & ~(kKT - 1);
+    RawTile TA, TB;
+    load_glb(tfirst, TA);
+    load_glb(min(tfirst + kKT, tlast), TB);
+    load_q();
+    stage_any(tfirst, TA, 0);
+    load_glb(min(tfirst + 2 * kKT, tlast), TA);
+    // At the barrier every wave has staged tile t0 into buffer ob and is done multiplying the previous tile from
+    // buffer ob ^ 1, which then takes tile t0 + 64 (codes in Tn, which then takes the codes of tile t0 + 192).
+    auto step = [&](int t0, int ob, RawTile& Tn) __attribute__((always_inline)) {
+      barrier();
+      compute(t0, nullptr, ob);
+      if (t0 + kKT < khi) stage_any(t0 + kKT, Tn, ob ^ 1);
+      load_glb(min(t0 + 3 * kKT, tlast), Tn);
+    };
+    for (int t0 = tfirst;;) {
+      step(t0, 0, TB);
+      t0 += kKT;
+      if (t0 >= khi) break;
+      step(t0, 1, TA);
+      t0 += kKT;
+      if (t0 >= khi) break;
+    }
+  } else if constexpr (FMT == KV_Q8) {
     // s_waitcnt vmcnt(5) (the other slot's five loads of this wave may stay in flight), vmcnt(0), lgkmcnt(0)
     constexpr int kWaitOne = (0xF << 8) | (0x7 << 4) | 5;
     constexpr int kWaitAll = (0xF << 8) | (0x7 << 4);
@@ -547,11 +603,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       barrier();  // the slot's tile is in LDS; every wave is done with the previous tile's operands
       RawTile T;
       load_lds(S, T);
-      if (t0 >= klo && t0 + kKT <= khi) stage(t0, T, std::false_type{});
-      else stage(t0, T, std::true_type{});
+      if (t0 >= klo && t0 + kKT <= khi) stage(t0, T, std::false_type{}, 0);
+      else stage(t0, T, std::true_type{}, 0);
       barrier();  // operands ready; the slot is free
       if (t0 + 2 * kKT < khi) dma(t0 + 2 * kKT, S);
-      compute(t0, S);
+      compute(t0, S, 0);
     };
     dma(tfirst, raw0);
     if (tfirst + kKT < khi) dma(tfirst + kKT, raw1);
@@ -606,7 +662,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         clear_v(t0, S);
         barrier();
       }
-      compute(t0, S);
+      compute(t0, S, 0);
     };
     dma16t(tfirst, raw0);
     load_q();
