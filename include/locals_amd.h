@@ -36,7 +36,8 @@ enum { LCL_OK = 0, LCL_EINVAL = -1, LCL_EUNSUPPORTED = -2, LCL_EWORKSPACE = -3, 
 
 /* Bytes of split-K workspace for R query rows of H heads over `extent` keys
  * (n for lcl_qkv_attend, cap for lcl_ragged_attention) with key chunk `block`
- * (0 = the library's choice; otherwise a multiple of 64). */
+ * (0 = the library's choice; otherwise a multiple of 64): m, l and o[128] in fp32 for
+ * every part of every (row, head), then one int32 part count a (row, head). */
 size_t lcl_decode_workspace_bytes(int R, int H, int extent, int block);
 
 /* qkv.attend (locals/qkv.py:213-249): one query per row against 8-bit affine

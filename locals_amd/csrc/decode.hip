@@ -77,6 +77,7 @@ struct DecodeParams {
   float* pm;
   float* pl;
   float* po;
+  int32_t* qparts;  // quad pass 1: parts of each (row, kv head) stream, written by the wave holding its first tile
   int n, cap, H, KVH, G, nslices, nchunks, chunk;
   int kv_rows;  // rows of the KV buffers (B, or n_slots); a slot outside is clamped
   int R;        // query rows
@@ -96,8 +97,8 @@ struct CombineParams {
   const int32_t* start;
   const int32_t* nkeys;
   int n, cap, H, nchunks, chunk, odt;
-  int quad, R, KVH, G, qwaves, qmint;  // quad: parts are the stream-K slots of the quad pass 1
-  int qwa, qwb, qya, qyb, qold;
+  int quad, R, KVH, G;  // quad: parts are the stream-K slots of the quad pass 1, counted in qparts
+  const int32_t* qparts;
 };
 
 __device__ __forceinline__ void row_range(const int32_t* start, const int32_t* nkeys, int n, int cap, int r, int& lo,
@@ -492,7 +493,7 @@ __device__ __forceinline__ uint32_t row_take2(uint32_t x0, uint32_t x1) {
 //    issue favours; the younger ones took ~22% longer a tile.
 // Weights: even old a, odd old b, even young c, odd young d (SplitW).  A wave writes one partial
 // for each (row, kv head) stream its range touches, at slot j = wave - (wave holding the
-// stream's first tile); pass 2 recomputes the same split.
+// stream's first tile); that first wave also records the stream's part count for pass 2.
 struct SplitW {
   int a, b, c, d, old;  // old: even
 };
@@ -1074,6 +1075,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void
       wb1[e] += __shfl_xor(wb1[e], 32);
     }
     const int jslot = wv - quad_wave_of(cur.Gs, T, W, sw);
+    if (jslot == 0 && lane == 0)  // the stream's parts run from this wave to the one holding its last tile
+      p.qparts[cur.r * p.KVH + cur.kvh] = quad_wave_of(cur.Gs + cur.cnt - 1, T, W, sw) - wv + 1;
     // lanes of quad q4 < HG write head group q4: row i of O is head 4 q4 + i
     if (q4 < HG) {
       const int e = HG == 1 ? 0 : q4;
@@ -1318,21 +1321,14 @@ __global__ __launch_bounds__(256) void decode_combine(CombineParams p) {
     l0 = p.pl[base + cs];
     o0 = po4[(base + cs) * (kHD / 4)];
   }
+  // quad: the stream's part count as pass 1 recorded it, loaded beside the first part (read only for a row with
+  // keys: no wave writes the count of an empty stream)
+  const int qp = p.quad ? p.qparts[r * p.KVH + head / p.G] : 0;
   int lo, hi;
   row_range(p.start, p.nkeys, p.n, p.cap, r, lo, hi);
   int cl = 0, ch = 0;
   if (p.quad) {
-    long long T, before;
-    int W;
-    SplitW sw{p.qwa, p.qwb, p.qya, p.qyb, p.qold};
-    quad_split(p.start, p.nkeys, p.n, p.cap, p.R, p.KVH, p.qwaves, p.qmint, sw, T, W, r, before);
-    const long long acc_t = before * p.KVH;
-    int t0, l2, h2;
-    const int cnt = quad_row_tiles(p.start, p.nkeys, p.n, p.cap, r, t0, l2, h2);
-    if (cnt > 0) {
-      const long long Gs = acc_t + (long long)(head / p.G) * cnt;
-      ch = quad_wave_of(Gs + cnt - 1, T, W, sw) - quad_wave_of(Gs, T, W, sw) + 1;
-    }
+    if (hi > lo) ch = qp;
   } else if (hi > lo) {
     cl = lo / p.chunk;
     ch = (hi + p.chunk - 1) / p.chunk;
@@ -1470,7 +1466,8 @@ static int pick_chunk(int block, int extent) {
 }
 
 static size_t ws_bytes_for(int R, int H, int nchunks) {
-  return size_t(R) * H * nchunks * (2 + kHD) * sizeof(float);
+  // m, l and o of every part, then one part count a (row, head) (the quad pass 1's streams)
+  return size_t(R) * H * nchunks * (2 + kHD) * sizeof(float) + size_t(R) * H * sizeof(int32_t);
 }
 
 // quad pass 1: least keys a wave = the block (a multiple of 64); slots a (row, head) for `extent` keys
@@ -1644,6 +1641,7 @@ int lcl_qkv_attend_ex(const void* q, int qdt, const uint32_t* kw, const void* ks
   p.pm = ws;
   p.pl = ws + np;
   p.po = ws + 2 * np;
+  p.qparts = reinterpret_cast<int32_t*>(ws + (2 + kHD) * np);
   p.n = n; p.cap = cap; p.H = H; p.KVH = KVH; p.kv_rows = B; p.R = B;
   p.nslices = (p.G + 15) / 16;
   p.nchunks = nparts; p.chunk = chunk;
@@ -1663,8 +1661,7 @@ int lcl_qkv_attend_ex(const void* q, int qdt, const uint32_t* kw, const void* ks
   CombineParams c{};
   c.pm = p.pm; c.pl = p.pl; c.po = p.po; c.sinks = sinks; c.out = out;
   c.start = start; c.nkeys = nullptr; c.n = n; c.cap = cap; c.H = H; c.nchunks = nparts; c.chunk = chunk; c.odt = qdt;
-  c.quad = quad; c.R = B; c.KVH = KVH; c.G = p.G; c.qwaves = p.qwaves; c.qmint = p.qmint;
-  c.qwa = p.qwa; c.qwb = p.qwb; c.qya = p.qya; c.qyb = p.qyb; c.qold = p.qold;
+  c.quad = quad; c.R = B; c.KVH = KVH; c.G = p.G; c.qparts = p.qparts;
   hipLaunchKernelGGL(decode_combine, dim3(B * H, comb_slices(B * H)), dim3(256), 0, stream, c);
   return int(hipGetLastError());
 }

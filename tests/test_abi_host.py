@@ -70,8 +70,9 @@ def test_entry_points_reject_bad_arguments_without_a_gpu():
     assert rc == -4
     rc = lib.lcl_quantize_append(one, None, 0, one, one, one, None, None, None, 1, 1, 4, 100, 8, 0, 0, None)
     assert rc == -1  # D not a multiple of 64
-    # parts a (row, head): max(key chunks of 512, stream-K slots: ceil(16 tiles / 8 a wave) + 1) = 3
-    assert lib.lcl_decode_workspace_bytes(2, 4, 1000, 512) == 2 * 4 * 3 * (2 + 128) * 4
+    # parts a (row, head): max(key chunks of 512, stream-K slots: ceil(16 tiles / 8 a wave) + 1) = 3, each with m, l
+    # and 128 o; then one int32 part count a (row, head)
+    assert lib.lcl_decode_workspace_bytes(2, 4, 1000, 512) == 2 * 4 * 3 * (2 + 128) * 4 + 2 * 4 * 4
     # qk_norm_rope: head_dim 64 unsupported; f32 unsupported; null q invalid; H not a multiple of KV invalid;
     # an empty call (B * L == 0) is a no-op even with null pointers; the fused store past the capacity is invalid
     qk = lambda qkv, dt, H, KV, hd, B=1, L=1, q=one: lib.lcl_qk_norm_rope(qkv, dt, one, one, one, 0, 1e-6, 13.3, 1, B, L,
