@@ -15,8 +15,10 @@
 //
 // MI355X design.  Work units (key chunk, row block, batch row x kv head), dealt to the
 // XCDs in contiguous runs; a workgroup = 4 waves = 64 or 128 rows (one or two 16-row
-// tiles a wave), a row being one (query, head) of the kv head's G heads (row r: query
-// r / G, head r % G, so any G works).  Per 64-key tile: 8-bit K and V are dequantized
+// tiles a wave), or 8 waves = 256 rows for 16-bit K/V with two row tiles (causal or no
+// mask: one workgroup a CU, each tile loaded into LDS serving twice the rows), a row
+// being one (query, head) of the kv head's G heads (row r: query r / G, head r % G, so
+// any G works).  Per 64-key tile: 8-bit K and V are dequantized
 // once into LDS as MFMA operands (fp32 scale * code + bias, rounded once to the MFMA
 // type, as the reference's dequantized() feeds its attention in T); 16-bit tiles are the
 // operands as loaded.  Every wave reuses the tile for its rows:
@@ -83,6 +85,7 @@ struct SdpaParams {
   int window;  // MK_WINDOW: keys a query sees, itself included
   void* out;  // direct: one chunk covers every key, so pass 1 writes the normalized output (B, H, L, 128), dtype odt
   int direct, odt;
+  int nw;  // waves a workgroup: 8 for 16-bit K/V with two row tiles (causal or no mask), else 4
 };
 
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
@@ -155,8 +158,9 @@ __device__ __forceinline__ uint2 lds_read_tr16(const uint8_t* p) {
 // tile is dequantized into the operand buffer and multiplied; one row tile: the codes arrive in registers two tiles
 // ahead and are dequantized into one of two operand buffers while the other's tile is multiplied.  16-bit: the K and V tiles arrive in one of two slots and
 // are multiplied in place while the next tile's loads are in flight.
-template <int QDT, int SDT, int FMT, int MT, int MASK, int RT>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void sdpa_pass1(SdpaParams p) {
+template <int QDT, int SDT, int FMT, int MT, int MASK, int RT, int NW = 4>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2))) void sdpa_pass1(SdpaParams p) {
+  static_assert(NW == 4 || (NW == 8 && FMT == KV_16 && RT == 2), "eight-wave workgroups: 16-bit K/V, two row tiles");
   // XCD-aware order: the hardware deals workgroups to the 8 XCDs round-robin, so physical workgroup P runs on
   // XCD P % 8; logical workgroup (P % 8) * ceil(total / 8) + P / 8 gives each XCD a contiguous run of (chunk,
   // row block, batch row x kv head) -- the same kv head's K/V for all of it, which its own L2 then holds
@@ -169,18 +173,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63, tid = threadIdx.x;
   const int c16 = lane & 15, q4 = lane >> 4;
   const int R = p.L * p.G;
-  const int row0 = 64 * RT * rb;
-  // this lane's rows (one a row tile): r-th tile rows row0 + 64 r + 16 wave + [0, 16)
+  const int row0 = 16 * NW * RT * rb;
+  // this lane's rows (one a row tile): r-th tile rows row0 + 16 NW r + 16 wave + [0, 16)
   int rowi[RT], qi[RT], head[RT];
   bool real[RT];
 #pragma unroll
   for (int r = 0; r < RT; r++) {
-    rowi[r] = row0 + 64 * r + 16 * wave + c16;
+    rowi[r] = row0 + 16 * NW * r + 16 * wave + c16;
     real[r] = rowi[r] < R;
     qi[r] = real[r] ? rowi[r] / p.G : 0;
     head[r] = kvh * p.G + (real[r] ? rowi[r] % p.G : 0);
   }
-  const int last_q = min(R - 1, row0 + 64 * RT - 1) / p.G;
+  const int last_q = min(R - 1, row0 + 16 * NW * RT - 1) / p.G;
   const int wave_q0 = (row0 + 16 * wave) / p.G;  // the smallest query index among this wave's rows
   const int slo = p.start ? max(p.start[b], 0) : 0;
   // keys the workgroup's rows can see: [blo, bhi); chunks are counted from base (the band's first tile for a
@@ -442,7 +446,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     if constexpr (MASK == MK_TREE) full = full && t0 + kKT <= p.N - p.L;
     if constexpr (MASK == MK_WINDOW)  // causal for the wave's first query, in the window of its last
       full = full && t0 + kKT - 1 <= p.N - p.L + wave_q0 &&
-             t0 > p.N - p.L + (row0 + 64 * (RT - 1) + 16 * wave + 15) / p.G - p.window;
+             t0 > p.N - p.L + (row0 + 16 * NW * (RT - 1) + 16 * wave + 15) / p.G - p.window;
     if constexpr (MASK == MK_DENSE) full = false;
     if constexpr (kStepOuter) {
       // The mask enters as the accumulators' initial value (-m_run or -inf), so the scores need no pass after the
@@ -621,7 +625,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       if (t0 >= khi) break;
     }
   } else {
-    // 16-bit: wave w loads key rows 16 w .. 16 w + 15 of K and of V (4 instructions of 1 KB each), chunk c of
+    // 16-bit: wave w loads key rows 64 / NW w .. of K and of V (16 / NW instructions of 1 KB each), chunk c of
     // row r to slot c ^ swk(r) (K) or c ^ swv(r) (V)
     constexpr int kWaitAll = (0xF << 8) | (0x7 << 4);
     constexpr int kWaitLds = (0x3 << 14) | (0x7 << 4) | 0xF;
@@ -632,23 +636,24 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     };
     auto dma16t = [&](int t0, uint8_t* S) __attribute__((always_inline)) {
       const uint32_t ls = lds_addr(S);
+      constexpr int kPieces = 16 / NW;  // 1 KB pieces (4 key rows) of K and of V a wave sends
 #pragma unroll
-      for (int u = 0; u < 4; u++) {
-        const int r = 16 * wave + 4 * u + (lane >> 4);
+      for (int u = 0; u < kPieces; u++) {
+        const int r = 4 * kPieces * wave + 4 * u + (lane >> 4);
         const uint32_t voff = uint32_t(t0 + r) * 256u + 16u * uint32_t(lane & 15);
-        dma16(dk16, ls + 1024u * uint32_t(4 * wave + u), voff ^ (16u * uint32_t(swk(r))));
-        dma16(dv16, ls + 16384u + 1024u * uint32_t(4 * wave + u), voff ^ (16u * uint32_t(swv(r))));
+        dma16(dk16, ls + 1024u * uint32_t(kPieces * wave + u), voff ^ (16u * uint32_t(swk(r))));
+        dma16(dv16, ls + 16384u + 1024u * uint32_t(kPieces * wave + u), voff ^ (16u * uint32_t(swv(r))));
       }
     };
     // a tile reaching past [klo, khi): the K and V rows of keys outside it are cleared (rows past n or before
     // start may hold anything, 0 * inf is not 0, and a masked score starts at -inf, which a NaN product would undo)
     auto clear_v = [&](int t0, uint8_t* S) __attribute__((always_inline)) {
-      const int key = tid >> 2, kg = t0 + key;
+      const int key = tid / NW, kg = t0 + key;  // NW threads a key row, 256 / NW bytes each
       if (kg < klo || kg >= khi) {
-        uint4* row = reinterpret_cast<uint4*>(S + 16384 + key * 256 + 64 * (tid & 3));
-        uint4* krow = reinterpret_cast<uint4*>(S + key * 256 + 64 * (tid & 3));
+        uint4* row = reinterpret_cast<uint4*>(S + 16384 + key * 256 + (256 / NW) * (tid % NW));
+        uint4* krow = reinterpret_cast<uint4*>(S + key * 256 + (256 / NW) * (tid % NW));
 #pragma unroll
-        for (int i = 0; i < 4; i++) row[i] = krow[i] = make_uint4(0u, 0u, 0u, 0u);
+        for (int i = 0; i < 16 / NW; i++) row[i] = krow[i] = make_uint4(0u, 0u, 0u, 0u);
       }
     };
     // One barrier a tile: at its top every wave's loads of this tile are in slot S and every wave is done with
@@ -774,6 +779,12 @@ template <int QDT, int SDT, int FMT, int MT, int MASK>
 static void launch_rt(int rt, dim3 grid, hipStream_t s, hipEvent_t e0, hipEvent_t e1, const SdpaParams& p) {
   // two row tiles: 16-bit keys and values without a dense mask, 8-bit without a dense or window mask (their
   // per-key tests for two tiles would not fit beside the staging registers)
+  if constexpr (FMT == KV_16 && (MASK == MK_CAUSAL || MASK == MK_NONE || MASK == MK_WINDOW)) {
+    if (rt == 2 && p.nw == 8) {
+      hipExtLaunchKernelGGL((sdpa_pass1<QDT, SDT, FMT, MT, MASK, 2, 8>), grid, dim3(512), 0, s, e0, e1, 0, p);
+      return;
+    }
+  }
   if constexpr (MASK != MK_DENSE && (FMT == KV_16 || MASK != MK_WINDOW)) {
     if (rt == 2) {
       hipExtLaunchKernelGGL((sdpa_pass1<QDT, SDT, FMT, MT, MASK, 2>), grid, dim3(256), 0, s, e0, e1, 0, p);
@@ -814,13 +825,15 @@ static void launch_fmt(int qdt, int sdt, int rt, dim3 grid, hipStream_t s, hipEv
 using namespace lcl;
 
 // Keys a pass-1 workgroup reads: the caller's block, or enough chunks that the grid (about B H L / wg_rows row
-// blocks times the chunks) fills one resident round of ~512 workgroups -- no more: every extra chunk adds a
-// 520-byte part per row to write and read back.  One chunk (most prefill) writes the output directly.
-static int sdpa_chunk(int block, int B, int H, int L, int N, int wg_rows) {
+// blocks times the chunks) fills one resident round of `round` workgroups (~512 four-wave ones, two a CU; 256
+// eight-wave ones) -- no more: every extra chunk adds a 520-byte part per row to write and read back.  One chunk
+// (most prefill) writes the output directly.  For the same rows the eight-wave count never exceeds the four-wave
+// one: ceil(R / 128) <= 2 ceil(R / 256).
+static int sdpa_chunk(int block, int B, int H, int L, int N, int wg_rows, int round = 512) {
   if (block > 0) return block;
   const int tiles = max(1, (N + kKT - 1) / kKT);
   const long long rowblocks = max(1LL, ((long long)B * H * L + wg_rows - 1) / wg_rows);
-  const int want = int(min((long long)tiles, max(1LL, (512 + rowblocks - 1) / rowblocks)));
+  const int want = int(min((long long)tiles, max(1LL, (round + rowblocks - 1) / rowblocks)));
   return ((tiles + want - 1) / want) * kKT;
 }
 
@@ -930,6 +943,26 @@ int lcl_sdpa_ex(const void* q, int qdt, int kvfmt, const uint32_t* kw, const voi
     kf = kd;
     vf = vd;
   }
+  // 16-bit K/V with two row tiles, causal, windowed or unmasked: eight-wave workgroups of 256 rows, one a CU, so
+  // each K/V tile the workgroup loads into LDS serves twice the rows (C4's pass 1: 131.7 -> 123.7 us).  They are
+  // taken only where their chunk count is at most the four-wave one the workspace was checked for.
+  int nw = kvfmt == KV_16 && rt == 2 &&
+                   (mask_kind == MK_CAUSAL || mask_kind == MK_NONE || mask_kind == MK_WINDOW) ? 8 : 4;
+  if (nw == 8 && N > 0) {
+    int c8 = sdpa_chunk(block, B, H, L, N, 256, 256);
+    int n8 = (N + c8 - 1) / c8;
+    if (mask_kind == MK_WINDOW) {  // as above, for a 256-row workgroup's band
+      const long long ext = min((long long)N, (long long)window + 255 / (H / KVH) + kKT);
+      c8 = max(c8, sdpa_chunk(block, B, H, L, int(ext), 256, 256));
+      n8 = int((ext + c8 - 1) / c8);
+    }
+    if (n8 <= nchunks) {
+      chunk = c8;
+      nchunks = n8;
+    } else {
+      nw = 4;
+    }
+  }
   SdpaParams p{};
   p.q = q;
   p.kw = kw; p.ks = ks; p.kb = kb; p.vw = vw; p.vs = vs; p.vb = vb; p.kf = kf; p.vf = vf;
@@ -944,7 +977,8 @@ int lcl_sdpa_ex(const void* q, int qdt, int kvfmt, const uint32_t* kw, const voi
   p.B = B; p.H = H; p.KVH = KVH; p.G = H / KVH; p.L = L; p.N = N; p.cap = cap;
   p.nchunks = nchunks; p.chunk = chunk; p.mask = mask_kind; p.window = window;
   p.direct = nchunks == 1; p.out = out; p.odt = qdt;
-  p.nrowblocks = (rows + 64 * rt - 1) / (64 * rt);
+  p.nw = nw;
+  p.nrowblocks = (rows + 16 * nw * rt - 1) / (16 * nw * rt);
   {  // with no key in reach every workgroup records empty parts, so the combine needs no cleared workspace
     const long long total = (long long)nchunks * p.nrowblocks * B * KVH;  // one-dimensional, mapped per XCD
     if (total > (1LL << 30)) return -2;
