@@ -434,10 +434,10 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
     return ok;
   };
   auto compute = [&](int t0, const uint8_t* S, int ob) __attribute__((always_inline)) {
-    // S^T = K Q^T: st[r][t][i] = S[row][t0 + 16 t + 4 q4 + i].  Where registers allow (causal mask, one row
-    // tile), the 32-dim step kk is the outer loop, so the 4 RT accumulators are independent chains and a step's
-    // four K fragments are read together; otherwise a key block t at a time.
-    constexpr bool kStepOuter = MASK == MK_CAUSAL || RT == 1;
+    // S^T = K Q^T: st[r][t][i] = S[row][t0 + 16 t + 4 q4 + i].  Where registers allow (causal and window masks,
+    // one row tile), the 32-dim step kk is the outer loop, so the 4 RT accumulators are independent chains and a
+    // step's four K fragments are read together; otherwise a key block t at a time.
+    constexpr bool kStepOuter = MASK == MK_CAUSAL || MASK == MK_WINDOW || RT == 1;
     f4 st[RT][4];  // relative to m_run: every chain starts from negm
     // a tile every key of which every row of the wave sees needs no mask (for causal prefill, all but the
     // diagonal tiles); rows past the row count are not written, so they need none either
