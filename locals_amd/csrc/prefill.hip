@@ -15,10 +15,10 @@
 //
 // MI355X design.  Work units (key chunk, row block, batch row x kv head), dealt to the
 // XCDs in contiguous runs; a workgroup = 4 waves = 64 or 128 rows (one or two 16-row
-// tiles a wave), or 8 waves = 256 rows for 16-bit K/V with two row tiles (causal or no
-// mask: one workgroup a CU, each tile loaded into LDS serving twice the rows), a row
-// being one (query, head) of the kv head's G heads (row r: query r / G, head r % G, so
-// any G works).  Per 64-key tile: 8-bit K and V are dequantized
+// tiles a wave), or 8 waves = 256 rows with two row tiles under a causal or no mask (and a
+// window, 16-bit K/V): one workgroup a CU, each tile loaded and staged in LDS serving twice
+// the rows; a row being one (query, head) of the kv head's G heads (row r: query r / G,
+// head r % G, so any G works).  Per 64-key tile: 8-bit K and V are dequantized
 // once into LDS as MFMA operands (fp32 scale * code + bias, rounded once to the MFMA
 // type, as the reference's dequantized() feeds its attention in T); 16-bit tiles are the
 // operands as loaded.  Every wave reuses the tile for its rows:
@@ -160,7 +160,7 @@ __device__ __forceinline__ uint2 lds_read_tr16(const uint8_t* p) {
 // are multiplied in place while the next tile's loads are in flight.
 template <int QDT, int SDT, int FMT, int MT, int MASK, int RT, int NW = 4>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2))) void sdpa_pass1(SdpaParams p) {
-  static_assert(NW == 4 || (NW == 8 && FMT == KV_16 && RT == 2), "eight-wave workgroups: 16-bit K/V, two row tiles");
+  static_assert(NW == 4 || (NW == 8 && RT == 2), "eight-wave workgroups: two row tiles");
   // XCD-aware order: the hardware deals workgroups to the 8 XCDs round-robin, so physical workgroup P runs on
   // XCD P % 8; logical workgroup (P % 8) * ceil(total / 8) + P / 8 gives each XCD a contiguous run of (chunk,
   // row block, batch row x kv head) -- the same kv head's K/V for all of it, which its own L2 then holds
@@ -278,32 +278,46 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
   const sg4 dk16 = rsrc_words(static_cast<const uint16_t*>(FMT == KV_16 ? p.kf : p.kw) + tok0 * kD, cap * 256u);
   const sg4 dv16 = rsrc_words(static_cast<const uint16_t*>(FMT == KV_16 ? p.vf : p.vw) + tok0 * kD, cap * 256u);
   // 8-bit DMA: the scale / bias array this wave sends (wave 0 K scales, 1 K biases, 2 V scales, 3 V biases)
-  const void* sarr = FMT != KV_Q8 ? p.kf : wave == 0 ? p.ks : wave == 1 ? p.kb : wave == 2 ? p.vs : p.vb;
+  const int warr = wave & 3;  // eight waves: waves w and w + 4 send the two halves of array w
+  const void* sarr = FMT != KV_Q8 ? p.kf : warr == 0 ? p.ks : warr == 1 ? p.kb : warr == 2 ? p.vs : p.vb;
   const BufRsrc rsw = make_rsrc(static_cast<const uint16_t*>(sarr) + tok0 * 2, cap * 4u);
-  const int kkey = tid >> 2, kpart = tid & 3;   // staging: one key, 32 dims of its K and V
+  const int kkey = tid / NW, kpart = tid % NW;   // staging: one key, 128 / NW dims of its K and V
 
   // 8-bit raw tile in LDS: K codes (key-major 128 B rows, 8 KB), V codes (8 KB), ks / kb / vs / vb words (256 B
   // each).  Wave w sends K and V rows 16 w .. 16 w + 15 (two 1 KB pieces each) and the w-th scale array.  Row r
   // keeps its 16-byte chunk c at slot c ^ ((r >> 1) & 1), so the staging reads (32 bytes of each of 16 rows a
   // wave) cover every bank group.
   auto dma = [&](int t0, uint8_t* S) __attribute__((always_inline)) {
+    constexpr int kRowsW = 64 / NW;  // key rows a wave sends, 8 a 1 KB piece
 #pragma unroll
-    for (int i = 0; i < 2; i++) {
-      const int r = 16 * wave + 8 * i + (lane >> 3);
+    for (int i = 0; i < kRowsW / 8; i++) {
+      const int r = kRowsW * wave + 8 * i + (lane >> 3);
       const uint32_t voff = uint32_t(t0 + r) * 128u + 16u * uint32_t((lane & 7) ^ ((r >> 1) & 1));
-      lds_load16<0>(rk, S + 2048 * wave + 1024 * i, voff);
-      lds_load16<0>(rv, S + 8192 + 2048 * wave + 1024 * i, voff);
+      lds_load16<0>(rk, S + 128 * kRowsW * wave + 1024 * i, voff);
+      lds_load16<0>(rv, S + 8192 + 128 * kRowsW * wave + 1024 * i, voff);
     }
-    lds_load4<0>(rsw, S + 16384 + 256 * wave, (uint32_t(t0) + uint32_t(lane)) * 4u);
+    if constexpr (NW == 4) {
+      lds_load4<0>(rsw, S + 16384 + 256 * wave, (uint32_t(t0) + uint32_t(lane)) * 4u);
+    } else if (lane < 32) {
+      const int h = wave >> 2;
+      lds_load4<0>(rsw, S + 16384 + 256 * warr + 128 * h, (uint32_t(t0 + 32 * h) + uint32_t(lane)) * 4u);
+    }
   };
   // the thread's share of a raw tile in LDS, as the register-prefetch path would hold it
   auto load_lds = [&](const uint8_t* S, RawTile& T) __attribute__((always_inline)) {
-    const int f = (kkey >> 1) & 1;  // the row's chunk swizzle: chunks 2 kpart, 2 kpart + 1 at slots c ^ f
-    const uint8_t* kr = S + kkey * 128 + 32 * kpart;
-    T.k[0] = *reinterpret_cast<const u4*>(kr + 16 * f);
-    T.k[1] = *reinterpret_cast<const u4*>(kr + 16 * (f ^ 1));
-    T.v[0] = *reinterpret_cast<const u4*>(kr + 8192 + 16 * f);
-    T.v[1] = *reinterpret_cast<const u4*>(kr + 8192 + 16 * (f ^ 1));
+    const int f = (kkey >> 1) & 1;  // the row's chunk swizzle: chunk c at slot c ^ f
+    if constexpr (NW == 4) {  // chunks 2 kpart, 2 kpart + 1
+      const uint8_t* kr = S + kkey * 128 + 32 * kpart;
+      T.k[0] = *reinterpret_cast<const u4*>(kr + 16 * f);
+      T.k[1] = *reinterpret_cast<const u4*>(kr + 16 * (f ^ 1));
+      T.v[0] = *reinterpret_cast<const u4*>(kr + 8192 + 16 * f);
+      T.v[1] = *reinterpret_cast<const u4*>(kr + 8192 + 16 * (f ^ 1));
+    } else {  // chunk kpart
+      const uint8_t* kr = S + kkey * 128 + 16 * (kpart ^ f);
+      T.k[0] = *reinterpret_cast<const u4*>(kr);
+      T.v[0] = *reinterpret_cast<const u4*>(kr + 8192);
+      T.k[1] = T.v[1] = u4{0u, 0u, 0u, 0u};  // not read: a thread stages one 16-byte chunk
+    }
     T.ks = *reinterpret_cast<const uint32_t*>(S + 16384 + 4 * kkey);
     T.kb = *reinterpret_cast<const uint32_t*>(S + 16640 + 4 * kkey);
     T.vs = *reinterpret_cast<const uint32_t*>(S + 16896 + 4 * kkey);
@@ -323,21 +337,22 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
   };
 
   // dequantize 32 codes (dims 32 kpart ..) with the key's scale / bias pair: 16 packed pairs of the MFMA type
+  constexpr int kW = 32 / NW;  // code words a thread stages of a key's K (and of its V)
   auto dequant = [&](const u4 (&c)[2], uint32_t sc, uint32_t bi, uint32_t (&o)[16]) __attribute__((always_inline)) {
     const uint32_t cw[8] = {c[0].x, c[0].y, c[0].z, c[0].w, c[1].x, c[1].y, c[1].z, c[1].w};
-    const int gsel = kpart >> 1;  // group of dims 32 kpart .. + 32
+    const int gsel = kpart / (NW / 2);  // group of the thread's dims (128 / NW kpart ..)
     if constexpr (MT == DT_F16) {
       const uint32_t s1 = (sc >> (16 * gsel)) & 0xffffu, b1 = (bi >> (16 * gsel)) & 0xffffu;
       const uint32_t s2 = s1 | (s1 << 16), b2 = b1 | (b1 << 16);
 #pragma unroll
-      for (int w = 0; w < 8; w++) {
+      for (int w = 0; w < kW; w++) {
         o[2 * w] = dq_h2(codes_to_h2(cw[w], 0x00050004u), s2, b2);
         o[2 * w + 1] = dq_h2(codes_to_h2(cw[w], 0x00070006u), s2, b2);
       }
     } else {
       const float sf = half_of(sc, gsel, SDT), bf = half_of(bi, gsel, SDT);
 #pragma unroll
-      for (int w = 0; w < 8; w++) {
+      for (int w = 0; w < kW; w++) {
         o[2 * w] = pack2<MT>(sf * float(cw[w] & 0xffu) + bf, sf * float((cw[w] >> 8) & 0xffu) + bf);
         o[2 * w + 1] = pack2<MT>(sf * float((cw[w] >> 16) & 0xffu) + bf, sf * float(cw[w] >> 24) + bf);
       }
@@ -352,15 +367,15 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
     const bool kin = !MASKED || (kg >= klo && kg < khi);
     uint32_t o[16];
     dequant(T.k, T.ks, T.kb, o);
-    uint4* kdst = reinterpret_cast<uint4*>(&Ks[ob * (kKT * kKsStride) + kkey * kKsStride + kpart * 32]);
+    uint4* kdst = reinterpret_cast<uint4*>(&Ks[ob * (kKT * kKsStride) + kkey * kKsStride + kpart * (128 / NW)]);
 #pragma unroll
-    for (int u = 0; u < 4; u++)
+    for (int u = 0; u < kW / 2; u++)
       kdst[u] = kin ? make_uint4(o[4 * u], o[4 * u + 1], o[4 * u + 2], o[4 * u + 3]) : make_uint4(0u, 0u, 0u, 0u);
     dequant(T.v, T.vs, T.vb, o);
     const int sw = swv(kkey);
 #pragma unroll
-    for (int u = 0; u < 4; u++)
-      *reinterpret_cast<uint4*>(&Vk[ob * (kKT * 256) + kkey * 256 + 16 * ((4 * kpart + u) ^ sw)]) =
+    for (int u = 0; u < kW / 2; u++)
+      *reinterpret_cast<uint4*>(&Vk[ob * (kKT * 256) + kkey * 256 + 16 * (((kW / 2) * kpart + u) ^ sw)]) =
           kin ? make_uint4(o[4 * u], o[4 * u + 1], o[4 * u + 2], o[4 * u + 3]) : make_uint4(0u, 0u, 0u, 0u);
   };
 
@@ -592,7 +607,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
     }
   } else if constexpr (FMT == KV_Q8) {
     // s_waitcnt vmcnt(5) (the other slot's five loads of this wave may stay in flight), vmcnt(0), lgkmcnt(0)
-    constexpr int kWaitOne = (0xF << 8) | (0x7 << 4) | 5;
+    constexpr int kWaitOne = (0xF << 8) | (0x7 << 4) | (NW == 4 ? 5 : 3);
     constexpr int kWaitAll = (0xF << 8) | (0x7 << 4);
     constexpr int kWaitLds = (0x3 << 14) | (0x7 << 4) | 0xF;
     // a workgroup barrier for LDS that leaves the other slot's loads in flight (__syncthreads would wait for them)
@@ -779,7 +794,8 @@ template <int QDT, int SDT, int FMT, int MT, int MASK>
 static void launch_rt(int rt, dim3 grid, hipStream_t s, hipEvent_t e0, hipEvent_t e1, const SdpaParams& p) {
   // two row tiles: 16-bit keys and values without a dense mask, 8-bit without a dense or window mask (their
   // per-key tests for two tiles would not fit beside the staging registers)
-  if constexpr (FMT == KV_16 && (MASK == MK_CAUSAL || MASK == MK_NONE || MASK == MK_WINDOW)) {
+  if constexpr ((FMT == KV_16 && (MASK == MK_CAUSAL || MASK == MK_NONE || MASK == MK_WINDOW)) ||
+                (FMT == KV_Q8 && (MASK == MK_CAUSAL || MASK == MK_NONE))) {
     if (rt == 2 && p.nw == 8) {
       hipExtLaunchKernelGGL((sdpa_pass1<QDT, SDT, FMT, MT, MASK, 2, 8>), grid, dim3(512), 0, s, e0, e1, 0, p);
       return;
@@ -845,14 +861,19 @@ static int sdpa_row_tiles(int rows, int mask_kind, int kvfmt) {
 }
 
 // Whether an 8-bit call dequantizes K and V once into the workspace and runs the 16-bit kernel over them.  The
-// fused kernel dequantizes every tile in each workgroup that reads it, i.e. once per row block of a (row, KV head);
-// from 16 row blocks one pass over the cache costs less (C4's 512-query causal chunk over 16k keys: 199 us fused
-// against 26.5 + 161 us).  Not under a window (a workgroup reads only its band of keys), nor when the buffers hold
-// many positions past N (the pass covers every position up to cap).
+// fused kernel dequantizes every tile in each workgroup that reads it, i.e. once per row block of a (row, KV head),
+// so past some number of row blocks one pass over the cache costs less.  With eight-wave workgroups (two row tiles,
+// causal or no mask: 256-row blocks) that is from 11 blocks: at C4 (8 blocks of 256 rows, 16k keys) the fused
+// kernel's staging cost 19.4 us over the 16-bit kernel's pass 1 against ~25 us for the dequantization (call 155.9
+// against 159.8 us), and the staging grows with the row blocks while the dequantization does not.  Otherwise
+// (64- or 128-row blocks) from 16 blocks (199 us fused against 26.5 + 161 us at C4 with four-wave workgroups).  Not
+// under a window (a workgroup reads only its band of keys), nor when the buffers hold many positions past N (the
+// pass covers every position up to cap).
 static bool sdpa_dequantize_first(int kvfmt, int mask_kind, int H, int KVH, int L, int N, int cap) {
   if (kvfmt != KV_Q8 || mask_kind == MK_WINDOW || N <= 0 || cap - N > 512) return false;
   const int rows = L * (H / KVH);
-  const int rt = sdpa_row_tiles(rows, mask_kind, KV_16);
+  const int rt = sdpa_row_tiles(rows, mask_kind, KV_Q8);
+  if (rt == 2 && (mask_kind == MK_CAUSAL || mask_kind == MK_NONE)) return (rows + 255) / 256 >= 11;
   return (rows + 64 * rt - 1) / (64 * rt) >= 16;
 }
 
@@ -943,11 +964,12 @@ int lcl_sdpa_ex(const void* q, int qdt, int kvfmt, const uint32_t* kw, const voi
     kf = kd;
     vf = vd;
   }
-  // 16-bit K/V with two row tiles, causal, windowed or unmasked: eight-wave workgroups of 256 rows, one a CU, so
-  // each K/V tile the workgroup loads into LDS serves twice the rows (C4's pass 1: 131.7 -> 123.7 us).  They are
-  // taken only where their chunk count is at most the four-wave one the workspace was checked for.
-  int nw = kvfmt == KV_16 && rt == 2 &&
-                   (mask_kind == MK_CAUSAL || mask_kind == MK_NONE || mask_kind == MK_WINDOW) ? 8 : 4;
+  // Two row tiles under a causal or no mask (and a window, 16-bit K/V): eight-wave workgroups of 256 rows, one a
+  // CU, so each K/V tile the workgroup loads (and, 8-bit, dequantizes) into LDS serves twice the rows (C4's 16-bit
+  // pass 1: 131.7 -> 123.7 us; its fused 8-bit pass 1: 167.1 -> 146.3 us).  They are taken only where their chunk
+  // count is at most the four-wave one the workspace was checked for.
+  int nw = rt == 2 && ((kvfmt == KV_16 && (mask_kind == MK_CAUSAL || mask_kind == MK_NONE || mask_kind == MK_WINDOW)) ||
+                        (kvfmt == KV_Q8 && (mask_kind == MK_CAUSAL || mask_kind == MK_NONE))) ? 8 : 4;
   if (nw == 8 && N > 0) {
     int c8 = sdpa_chunk(block, B, H, L, N, 256, 256);
     int n8 = (N + c8 - 1) / c8;

@@ -4,9 +4,9 @@ V groups with a common offset) and with the bench's N(0, 1) draws:
 
 * C3: one row, 16 / 8 heads, 245,760 keys of 8-bit K/V (split-K over ~256 waves a stream), vs the reference's
   two-pass split-K decode restated in C (locals/qkv.py:30-87, 179-208).
-* C4: the 512-query causal prompt chunk over 16,896 8-bit keys, 32 / 8 heads, through both routes (dequantize-first
-  and the fused 8-bit kernel), vs masked SDPA restated in C over the dequantized cache (locals/qkv.py:270-272);
-  and its 15 decode rows (contexts U[2k, 16k]).
+* C4: the 512-query causal prompt chunk over 16,896 8-bit keys, 32 / 8 heads (the fused 8-bit kernel, the route the
+  library takes there), and a 1024-query chunk over the same prefix (the dequantize-first route), vs masked SDPA
+  restated in C over the dequantized cache (locals/qkv.py:270-272); and C4's 15 decode rows (contexts U[2k, 16k]).
 * C5: 8 rows x 16 draft tokens in random trees (branching 1-3, depth <= 8) over 8,192 cached 8-bit keys, the
   ancestor-only mask (locals/treedec.py:56-67), vs the same C SDPA.
 Bar: 2e-3 max-abs (fp16 outputs)."""
@@ -58,14 +58,18 @@ def test_c3_full_size(dev, peaked):
     assert err <= 2e-3
 
 
-@pytest.mark.parametrize("route", ["dequantize-first", "fused-8bit"])
-def test_c4_prefill_full_size(dev, route):
-    from locals_amd import sdpa
+@pytest.mark.parametrize("route,L", [("fused-8bit", 512), ("dequantize-first", 1024)])
+def test_c4_prefill_full_size(dev, route, L):
+    from locals_amd import _lib, sdpa
 
-    B, H, KVH, L, P = 1, 32, 8, 512, 16384
+    B, H, KVH, P = 1, 32, 8, 16384
     N = P + L
     cap = (N + 255) // 256 * 256
-    print(f"C4 prefill full size, {route}", flush=True)
+    print(f"C4 prefill full size, {route}, L={L}", flush=True)
+    lib = _lib.load()
+    dq_room = lib.lcl_sdpa_workspace_bytes_kv(B, H, KVH, L, N, cap, sdpa.BLOCK, 0, sdpa.MASK_CAUSAL) > \
+        lib.lcl_sdpa_workspace_bytes(B, H, L, N, sdpa.BLOCK)
+    assert dq_room == (route == "dequantize-first")
     gen = torch.Generator(device=dev)
     gen.manual_seed(41)
     q, K, V = peaked_inputs_torch(gen, dev, B, H, KVH, L, cap, [0], [P], scale=SCALE, n_dom=3)

@@ -109,16 +109,17 @@ def test_sdpa_16bit(dev, kvdt, masked):
 
 @pytest.mark.parametrize("case", ["causal-float16", "dense-bfloat16"])
 def test_dequantize_first_route(dev, sdpa_block, case):
-    """8-bit K/V with 16 or more row blocks per (row, KV head): given the room (lcl_sdpa_workspace_bytes_kv) the
-    library dequantizes K and V once and runs the 16-bit kernel.  Its output equals the fused 8-bit kernel's bit for
+    """8-bit K/V with many row blocks per (row, KV head) (11 or more of 256 rows under a causal mask, 16 or more of
+    64 rows under a dense one): given the room (lcl_sdpa_workspace_bytes_kv) the library dequantizes K and V once
+    and runs the 16-bit kernel.  Its output equals the fused 8-bit kernel's bit for
     bit -- the same 16-bit operand values through the same products -- and the oracle within the bar, here with left
     padding and sinks."""
     from locals_amd import _lib, sdpa
 
     masked, dtype = case.split("-")
     g = rng(31 if masked == "causal" else 32)
-    if masked == "causal":  # 512 queries x 4 heads = 16 blocks of 128 rows
-        B, H, KVH, L, N = 1, 32, 8, 512, 700
+    if masked == "causal":  # 768 queries x 4 heads = 12 blocks of 256 rows
+        B, H, KVH, L, N = 1, 32, 8, 768, 900
     else:  # dense masks take 64-row blocks: 256 queries x 4 heads = 16
         B, H, KVH, L, N = 2, 16, 4, 256, 400
     cap = (N + 255) // 256 * 256
