@@ -95,6 +95,39 @@ def test_entry_points_reject_bad_arguments_without_a_gpu():
     assert sd(4, 0) == -1 and sd(4, -3) == -1 and sd(4, 5, L=11) == -1 and sd(5, 5) == -1
 
 
+def test_prompt_route_threshold_without_a_gpu():
+    """Where the library dequantizes 8-bit K/V once before the masked-attention pass (its workspace then has room
+    for the 16-bit copy): under a causal or no mask from 11 row blocks of 256 rows per (row, KV head), so C4's
+    512-query chunk (8 blocks) stays on the fused kernel; under a dense mask from 16 blocks of 64 rows; never under
+    a window, for 16-bit K/V, or when the buffers hold over 512 positions past N."""
+    from locals_amd import _lib, sdpa
+
+    lib = _lib.load()
+    B, H, KVH, P = 1, 32, 8, 16384
+
+    def dq(L, mk, kvfmt=0, extra_cap=0):
+        N = P + L
+        cap = (N + 255) // 256 * 256 + extra_cap
+        split = lib.lcl_sdpa_workspace_bytes(B, H, L, N, 0)
+        kv = lib.lcl_sdpa_workspace_bytes_kv(B, H, KVH, L, N, cap, 0, kvfmt, mk)
+        assert kv >= split
+        if kv > split:  # room for K and V as (B, KVH, cap, 128) 16-bit values after the split-K parts
+            assert kv >= split + 2 * B * KVH * cap * 128 * 2
+        return kv > split
+
+    causal, none, dense, window = sdpa.MASK_CAUSAL, sdpa.MASK_NONE, sdpa.MASK_DENSE, sdpa.MASK_WINDOW
+    assert not dq(512, causal)   # 2048 rows: 8 blocks of 256 (C4)
+    assert not dq(640, causal)   # 10 blocks
+    assert dq(704, causal)       # 2816 rows: 11 blocks
+    assert dq(1024, causal)      # 16 blocks
+    assert dq(704, none) and not dq(640, none)
+    assert dq(256, dense)        # 1024 rows: 16 blocks of 64
+    assert not dq(240, dense)    # 15 blocks
+    assert not dq(1024, window)
+    assert not dq(1024, causal, kvfmt=1)
+    assert not dq(1024, causal, extra_cap=768)
+
+
 def test_python_wrappers_refuse_cpu_tensors():
     from locals_amd import qkv
 
