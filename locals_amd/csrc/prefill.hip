@@ -860,10 +860,20 @@ static int sdpa_row_tiles(int rows, int mask_kind, int kvfmt) {
   return (rows > 64 && mask_kind != MK_DENSE && (kvfmt == KV_16 || mask_kind != MK_WINDOW)) ? 2 : 1;
 }
 
+// Eight-wave workgroups (256 rows, one a CU): two row tiles under a causal or no mask (and a window, 16-bit K/V),
+// and only where they add no padding rows over 128-row blocks -- the rows of a (row, KV head) a multiple of 256 or
+// more than 128 in the last block -- since every row of a block costs its products (a 32-query chunk at G = 4 would
+// otherwise compute 256 rows for 128).
+static bool sdpa_eight_waves(int rows, int mask_kind, int kvfmt) {
+  if (sdpa_row_tiles(rows, mask_kind, kvfmt) != 2) return false;
+  if (!(mask_kind == MK_CAUSAL || mask_kind == MK_NONE || (kvfmt == KV_16 && mask_kind == MK_WINDOW))) return false;
+  return rows % 256 == 0 || rows % 256 > 128;
+}
+
 // Whether an 8-bit call dequantizes K and V once into the workspace and runs the 16-bit kernel over them.  The
 // fused kernel dequantizes every tile in each workgroup that reads it, i.e. once per row block of a (row, KV head),
-// so past some number of row blocks one pass over the cache costs less.  With eight-wave workgroups (two row tiles,
-// causal or no mask: 256-row blocks) that is from 11 blocks: at C4 (8 blocks of 256 rows, 16k keys) the fused
+// so past some number of row blocks one pass over the cache costs less.  With eight-wave workgroups (256-row
+// blocks, sdpa_eight_waves) that is from 11 blocks: at C4 (8 blocks of 256 rows, 16k keys) the fused
 // kernel's staging cost 19.4 us over the 16-bit kernel's pass 1 against ~25 us for the dequantization (call 155.9
 // against 159.8 us), and the staging grows with the row blocks while the dequantization does not.  Otherwise
 // (64- or 128-row blocks) from 16 blocks (199 us fused against 26.5 + 161 us at C4 with four-wave workgroups).  Not
@@ -872,8 +882,8 @@ static int sdpa_row_tiles(int rows, int mask_kind, int kvfmt) {
 static bool sdpa_dequantize_first(int kvfmt, int mask_kind, int H, int KVH, int L, int N, int cap) {
   if (kvfmt != KV_Q8 || mask_kind == MK_WINDOW || N <= 0 || cap - N > 512) return false;
   const int rows = L * (H / KVH);
+  if (sdpa_eight_waves(rows, mask_kind, KV_Q8)) return (rows + 255) / 256 >= 11;
   const int rt = sdpa_row_tiles(rows, mask_kind, KV_Q8);
-  if (rt == 2 && (mask_kind == MK_CAUSAL || mask_kind == MK_NONE)) return (rows + 255) / 256 >= 11;
   return (rows + 64 * rt - 1) / (64 * rt) >= 16;
 }
 
@@ -964,12 +974,11 @@ int lcl_sdpa_ex(const void* q, int qdt, int kvfmt, const uint32_t* kw, const voi
     kf = kd;
     vf = vd;
   }
-  // Two row tiles under a causal or no mask (and a window, 16-bit K/V): eight-wave workgroups of 256 rows, one a
-  // CU, so each K/V tile the workgroup loads (and, 8-bit, dequantizes) into LDS serves twice the rows (C4's 16-bit
-  // pass 1: 131.7 -> 123.7 us; its fused 8-bit pass 1: 167.1 -> 146.3 us).  They are taken only where their chunk
-  // count is at most the four-wave one the workspace was checked for.
-  int nw = rt == 2 && ((kvfmt == KV_16 && (mask_kind == MK_CAUSAL || mask_kind == MK_NONE || mask_kind == MK_WINDOW)) ||
-                        (kvfmt == KV_Q8 && (mask_kind == MK_CAUSAL || mask_kind == MK_NONE))) ? 8 : 4;
+  // Eight-wave workgroups of 256 rows where sdpa_eight_waves allows them, one a CU, so each K/V tile the workgroup
+  // loads (and, 8-bit, dequantizes) into LDS serves twice the rows (C4's 16-bit pass 1: 131.7 -> 123.7 us; its
+  // fused 8-bit pass 1: 167.1 -> 146.3 us).  They are taken only where their chunk count is at most the four-wave
+  // one the workspace was checked for.
+  int nw = sdpa_eight_waves(rows, mask_kind, kvfmt) ? 8 : 4;
   if (nw == 8 && N > 0) {
     int c8 = sdpa_chunk(block, B, H, L, N, 256, 256);
     int n8 = (N + c8 - 1) / c8;

@@ -97,9 +97,10 @@ def test_entry_points_reject_bad_arguments_without_a_gpu():
 
 def test_prompt_route_threshold_without_a_gpu():
     """Where the library dequantizes 8-bit K/V once before the masked-attention pass (its workspace then has room
-    for the 16-bit copy): under a causal or no mask from 11 row blocks of 256 rows per (row, KV head), so C4's
-    512-query chunk (8 blocks) stays on the fused kernel; under a dense mask from 16 blocks of 64 rows; never under
-    a window, for 16-bit K/V, or when the buffers hold over 512 positions past N."""
+    for the 16-bit copy): with eight-wave workgroups (causal or no mask, rows a multiple of 256 or more than 128 in
+    the last 256-row block) from 11 row blocks of 256 rows per (row, KV head), so C4's 512-query chunk (8 blocks)
+    stays on the fused kernel; otherwise from 16 blocks of 128 (or, under a dense mask, 64) rows; never under a
+    window, for 16-bit K/V, or when the buffers hold over 512 positions past N."""
     from locals_amd import _lib, sdpa
 
     lib = _lib.load()
@@ -121,6 +122,10 @@ def test_prompt_route_threshold_without_a_gpu():
     assert dq(704, causal)       # 2816 rows: 11 blocks
     assert dq(1024, causal)      # 16 blocks
     assert dq(704, none) and not dq(640, none)
+    # rows leaving at most 128 in a last 256-row block keep four-wave workgroups (no padding rows added), and with
+    # them the 128-row threshold of 16 blocks
+    assert not dq(576, causal)   # 2304 rows: 9 blocks of 256, eight waves
+    assert dq(544, causal)       # 2176 rows: 17 blocks of 128, four waves
     assert dq(256, dense)        # 1024 rows: 16 blocks of 64
     assert not dq(240, dense)    # 15 blocks
     assert not dq(1024, window)
