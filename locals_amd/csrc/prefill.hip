@@ -987,7 +987,9 @@ int lcl_sdpa_ex(const void* q, int qdt, int kvfmt, const uint32_t* kw, const voi
       c8 = max(c8, sdpa_chunk(block, B, H, L, int(ext), 256, 256));
       n8 = int((ext + c8 - 1) / c8);
     }
-    if (n8 <= nchunks) {
+    // and only where their grid still fills the CUs (a short context leaves few chunks to split)
+    const long long grid8 = (long long)n8 * ((rows + 255) / 256) * B * KVH;
+    if (n8 <= nchunks && grid8 >= 256) {
       chunk = c8;
       nchunks = n8;
     } else {
