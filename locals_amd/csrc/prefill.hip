@@ -219,10 +219,11 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
   // transposing read).  16-bit: the K and V tiles arrive the same way
   // (chunks swizzled by swk / swv) and are the MFMA operands themselves -- K rows read as they are, V^T through the
   // transposing read -- so nothing is staged.
-  // 8-bit with one row tile: the codes come into registers two tiles ahead and there are two operand buffers
+  // 8-bit with one row tile, or in eight-wave workgroups: the codes come into registers two tiles ahead (32 or 16
+  // dims of a key's K and V a thread) and there are two operand buffers
   // (tile i multiplied from buffer i % 2 while tile i + 1 is staged into the other: one barrier a tile); the raw
   // slots are then unused
-  constexpr bool kRegPipe = FMT == KV_Q8 && RT == 1;
+  constexpr bool kRegPipe = FMT == KV_Q8 && (RT == 1 || NW == 8);
   constexpr int kOpBufs = kRegPipe ? 2 : 1;
   __shared__ __attribute__((aligned(16))) uint16_t Ks[FMT == KV_Q8 ? kOpBufs * kKT * kKsStride : 8];
   __shared__ __attribute__((aligned(16))) uint8_t Vk[FMT == KV_Q8 ? kOpBufs * kKT * 256 : 16];
@@ -325,11 +326,15 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
   };
   // the same share loaded from the buffers into registers (register pipeline)
   auto load_glb = [&](int t0, RawTile& T) __attribute__((always_inline)) {
-    const uint32_t key = uint32_t(t0 + kkey), co = key * 128u + 32u * uint32_t(kpart);
+    const uint32_t key = uint32_t(t0 + kkey), co = key * 128u + uint32_t(128 / NW) * uint32_t(kpart);
     T.k[0] = buf_load_b128(rk, co, 0);
-    T.k[1] = buf_load_b128(rk, co, 16);
     T.v[0] = buf_load_b128(rv, co, 0);
-    T.v[1] = buf_load_b128(rv, co, 16);
+    if constexpr (NW == 4) {
+      T.k[1] = buf_load_b128(rk, co, 16);
+      T.v[1] = buf_load_b128(rv, co, 16);
+    } else {
+      T.k[1] = T.v[1] = u4{0u, 0u, 0u, 0u};
+    }
     T.ks = buf_load_b32(rks, key * 4u, 0);
     T.kb = buf_load_b32(rkb, key * 4u, 0);
     T.vs = buf_load_b32(rvs, key * 4u, 0);
@@ -873,16 +878,16 @@ static bool sdpa_eight_waves(int rows, int mask_kind, int kvfmt) {
 // Whether an 8-bit call dequantizes K and V once into the workspace and runs the 16-bit kernel over them.  The
 // fused kernel dequantizes every tile in each workgroup that reads it, i.e. once per row block of a (row, KV head),
 // so past some number of row blocks one pass over the cache costs less.  With eight-wave workgroups (256-row
-// blocks, sdpa_eight_waves) that is from 11 blocks: at C4 (8 blocks of 256 rows, 16k keys) the fused
-// kernel's staging cost 19.4 us over the 16-bit kernel's pass 1 against ~25 us for the dequantization (call 155.9
-// against 159.8 us), and the staging grows with the row blocks while the dequantization does not.  Otherwise
-// (64- or 128-row blocks) from 16 blocks (199 us fused against 26.5 + 161 us at C4 with four-wave workgroups).  Not
-// under a window (a workgroup reads only its band of keys), nor when the buffers hold many positions past N (the
-// pass covers every position up to cap).
+// blocks, sdpa_eight_waves) that is from 12 blocks: at C4 (8 blocks of 256 rows, 16k keys) the fused kernel's
+// staging cost ~16.4 us over the 16-bit kernel's pass 1 (143.3 against 126.9 us) against ~25 us for the
+// dequantization and its launch, and the staging grows with the row blocks while the dequantization does not.
+// Otherwise (64- or 128-row blocks) from 16 blocks (199 us fused against 26.5 + 161 us at C4 with four-wave
+// workgroups).  Not under a window (a workgroup reads only its band of keys), nor when the buffers hold many
+// positions past N (the pass covers every position up to cap).
 static bool sdpa_dequantize_first(int kvfmt, int mask_kind, int H, int KVH, int L, int N, int cap) {
   if (kvfmt != KV_Q8 || mask_kind == MK_WINDOW || N <= 0 || cap - N > 512) return false;
   const int rows = L * (H / KVH);
-  if (sdpa_eight_waves(rows, mask_kind, KV_Q8)) return (rows + 255) / 256 >= 11;
+  if (sdpa_eight_waves(rows, mask_kind, KV_Q8)) return (rows + 255) / 256 >= 12;
   const int rt = sdpa_row_tiles(rows, mask_kind, KV_Q8);
   return (rows + 64 * rt - 1) / (64 * rt) >= 16;
 }
@@ -976,7 +981,7 @@ int lcl_sdpa_ex(const void* q, int qdt, int kvfmt, const uint32_t* kw, const voi
   }
   // Eight-wave workgroups of 256 rows where sdpa_eight_waves allows them, one a CU, so each K/V tile the workgroup
   // loads (and, 8-bit, dequantizes) into LDS serves twice the rows (C4's 16-bit pass 1: 131.7 -> 123.7 us; its
-  // fused 8-bit pass 1: 167.1 -> 146.3 us).  They are taken only where their chunk count is at most the four-wave
+  // fused 8-bit pass 1: 167.1 -> 143.3 us, its codes fed through registers).  They are taken only where their chunk count is at most the four-wave
   // one the workspace was checked for.
   int nw = sdpa_eight_waves(rows, mask_kind, kvfmt) ? 8 : 4;
   if (nw == 8 && N > 0) {

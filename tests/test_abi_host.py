@@ -98,7 +98,7 @@ def test_entry_points_reject_bad_arguments_without_a_gpu():
 def test_prompt_route_threshold_without_a_gpu():
     """Where the library dequantizes 8-bit K/V once before the masked-attention pass (its workspace then has room
     for the 16-bit copy): with eight-wave workgroups (causal or no mask, rows a multiple of 256 or more than 128 in
-    the last 256-row block) from 11 row blocks of 256 rows per (row, KV head), so C4's 512-query chunk (8 blocks)
+    the last 256-row block) from 12 row blocks of 256 rows per (row, KV head), so C4's 512-query chunk (8 blocks)
     stays on the fused kernel; otherwise from 16 blocks of 128 (or, under a dense mask, 64) rows; never under a
     window, for 16-bit K/V, or when the buffers hold over 512 positions past N."""
     from locals_amd import _lib, sdpa
@@ -118,10 +118,10 @@ def test_prompt_route_threshold_without_a_gpu():
 
     causal, none, dense, window = sdpa.MASK_CAUSAL, sdpa.MASK_NONE, sdpa.MASK_DENSE, sdpa.MASK_WINDOW
     assert not dq(512, causal)   # 2048 rows: 8 blocks of 256 (C4)
-    assert not dq(640, causal)   # 10 blocks
-    assert dq(704, causal)       # 2816 rows: 11 blocks
+    assert not dq(704, causal)   # 2816 rows: 11 blocks
+    assert dq(768, causal)       # 3072 rows: 12 blocks
     assert dq(1024, causal)      # 16 blocks
-    assert dq(704, none) and not dq(640, none)
+    assert dq(768, none) and not dq(704, none)
     # rows leaving at most 128 in a last 256-row block keep four-wave workgroups (no padding rows added), and with
     # them the 128-row threshold of 16 blocks
     assert not dq(576, causal)   # 2304 rows: 9 blocks of 256, eight waves

@@ -109,7 +109,7 @@ def test_sdpa_16bit(dev, kvdt, masked):
 
 @pytest.mark.parametrize("case", ["causal-float16", "dense-bfloat16"])
 def test_dequantize_first_route(dev, sdpa_block, case):
-    """8-bit K/V with many row blocks per (row, KV head) (11 or more of 256 rows under a causal mask, 16 or more of
+    """8-bit K/V with many row blocks per (row, KV head) (12 or more of 256 rows under a causal mask, 16 or more of
     64 rows under a dense one): given the room (lcl_sdpa_workspace_bytes_kv) the library dequantizes K and V once
     and runs the 16-bit kernel.  Its output equals the fused 8-bit kernel's bit for
     bit -- the same 16-bit operand values through the same products -- and the oracle within the bar, here with left
