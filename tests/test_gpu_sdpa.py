@@ -62,6 +62,31 @@ def test_causal_prefill_q8(dev, H, KVH, L, N):
 
 
 @pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
+def test_causal_prefill_q8_eight_waves(dev, sdpa_block, dtype):
+    """8-bit K/V, causal, 512 rows a (row, KV head) (128 queries x 4 heads): the fused kernel in eight-wave
+    workgroups of 256 rows, each thread feeding 16 dims of one key's K and V through registers, with left padding
+    and sinks, in fp16 and bf16, at every chunking."""
+    from locals_amd.sdpa import scaled_dot_product_attention
+
+    B, H, KVH, L, N = 2, 32, 8, 128, 1100
+    print(f"causal q8 eight waves {dtype} B={B} H={H} KVH={KVH} L={L} N={N} block={sdpa_block}", flush=True)
+    g = rng(211 if dtype == "float16" else 212)
+    cap = (N + 255) // 256 * 256
+    q = normal16(g, (B, H, L, 128), dtype=dtype)
+    K, V = q8_cache(g, B, KVH, cap, kscale=2.0, dtype=dtype)
+    sinks = normal16(g, (H,), 2.0, dtype=dtype)
+    start = np.array([0, 61], np.int32)
+    Kt, Vt = triple_to_torch(K, dev, dtype), triple_to_torch(V, dev, dtype)
+    got = scaled_dot_product_attention(to_torch(q, dev, dtype), tuple(a[:, :, :N] for a in Kt),
+                                       tuple(a[:, :, :N] for a in Vt), scale=0.0884, mask="causal",
+                                       sinks=to_torch(sinks, dev, dtype), start=to_torch(start, dev))
+    torch.cuda.synchronize()
+    vis = oa.causal_mask(L, N)[None, None] & (np.arange(N)[None, None, None, :] >= start[:, None, None, None])
+    ref = oa.sdpa_q8(q, K, V, 0.0884, vis, sinks, n=N, dtype=dtype)
+    assert np.abs(_np(got) - ref).max() <= _tol(ref, dtype)
+
+
+@pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
 def test_tree_verify_q8(dev, dtype):
     from locals_amd.sdpa import TreeMask, scaled_dot_product_attention
 
